@@ -1,0 +1,182 @@
+/*
+ * reng_hip.h - the C ABI of libreng_hip.so, the MI355X (gfx950) implementation
+ * of reng-fp8's per-output-channel FP8 weight quantizer and of the fused
+ * fp8-dequant GEMV / GEMM that consumes its codes.
+ *
+ * Plain C: pointers, sizes and integers only. Every device entry point takes
+ * an explicit stream (a hipStream_t passed as void*, NULL = the current
+ * device's null stream), is asynchronous on it, and keeps no hidden global
+ * stream. Every entry point is callable from any thread. On failure it returns
+ * a non-zero status and sets a thread-local message (reng_hip_last_error).
+ * There is no CPU fallback: a call that cannot run on the GPU fails.
+ *
+ * Data layout (the reference's, crates/reng-fp8/src/lib.rs:281-306):
+ *   weights  [rows, cols] row-major ([out, in]); bf16 bits or f32; row pitch ld
+ *            elements (ld >= cols; ld > cols takes a strided window)
+ *   codes    [rows, cols] row-major, one byte per element, pitch cols
+ *   scales   [rows] f32, weight[r, c] = decode(codes[r, c]) * scales[r]
+ */
+#ifndef RENG_HIP_H
+#define RENG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RENG_HIP_API __attribute__((visibility("default")))
+
+/* Status codes. */
+#define RENG_HIP_OK 0
+#define RENG_HIP_EINVAL 1      /* a shape, pointer, enum or backoff the reference would reject */
+#define RENG_HIP_EDEVICE 2     /* a HIP runtime error (launch, copy, no device) */
+#define RENG_HIP_ENOMEM 3      /* a device or pinned allocation failed */
+#define RENG_HIP_EUNSUPPORTED 4
+
+/* Fp8Format (crates/reng-fp8/src/lib.rs:53-58): E4M3 = Gaudi hf8, bias 7, max
+ * finite 240 (0x77); E5M2 = f8, bias 15, max finite 57344 (0x7b). */
+#define RENG_HIP_E4M3 0
+#define RENG_HIP_E5M2 1
+
+/* Scaling (crates/reng-fp8/src/lib.rs:240-256). */
+#define RENG_HIP_PCS 0   /* PerChannel: s[r] = absmax[r] / (max_finite * backoff), 1 for a zero row */
+#define RENG_HIP_HW 1    /* HwExpBias: one power of two from choose_exp_bias(tensor absmax / backoff) */
+#define RENG_HIP_UNIT 2  /* Unit: s = 1 */
+
+/* Element types of weights, activations and outputs. */
+#define RENG_HIP_BF16 0
+#define RENG_HIP_F32 1
+
+/* Library version string, e.g. "reng-hip 0.1.0 (gfx950)". */
+RENG_HIP_API const char *reng_hip_version(void);
+
+/* The message of the last failed call on this thread ("" if none). */
+RENG_HIP_API const char *reng_hip_last_error(void);
+
+/* One line describing the current device (name, gfx arch, CUs, HBM bytes,
+ * clock) written into buf. */
+RENG_HIP_API int reng_hip_device_info(char *buf, size_t len);
+
+/* ---------------------------------------------------------------------------
+ * Quantizer
+ * ------------------------------------------------------------------------- */
+
+/* reng_fp8::quantize_with (crates/reng-fp8/src/lib.rs:519-563), device-resident.
+ * w: dtype [rows, ld] (bf16 bits or f32), the first cols of each row are used.
+ * codes: [rows * cols] u8; scales: [rows] f32; exp_bias: optional device u32
+ * receiving the exponent bias of the device tensor's metadata (the chosen one
+ * for HW, the format's own otherwise). Codes and scales are bit-exact to the
+ * reference host quantizer on an x86 host, including NaN (sign | 0x7f), +-inf
+ * (saturated; inf inside a per-channel row gives s = inf, so finite entries
+ * encode to signed zero and inf/inf to 0xff, x86's negative default NaN) and
+ * zero rows (s = 1).
+ * Fails with EINVAL where quantize_with panics (lib.rs:527-532): rows or cols
+ * zero, backoff not positive and finite; also for ld < cols or NULL pointers. */
+RENG_HIP_API int reng_hip_quantize(const void *w, int dtype, size_t rows, size_t cols, size_t ld,
+                                   int format, int scaling, float backoff, uint8_t *codes,
+                                   float *scales, uint32_t *exp_bias, void *stream);
+
+/* The host-pointer form Rust's `quantize_with` calls: stages through device
+ * memory, runs reng_hip_quantize and copies back; synchronous. exp_bias is a
+ * host pointer (may be NULL). */
+RENG_HIP_API int reng_hip_quantize_host(const void *w, int dtype, size_t rows, size_t cols,
+                                        int format, int scaling, float backoff, uint8_t *codes,
+                                        float *scales, uint32_t *exp_bias);
+
+/* One matrix of a batch (device pointers); exp_bias may be NULL. */
+typedef struct reng_hip_matrix {
+    const void *w;
+    uint8_t *codes;
+    float *scales;
+    uint32_t *exp_bias;
+    size_t rows, cols, ld;
+} reng_hip_matrix;
+
+/* Many matrices, one format / scheme / backoff, as LlamaWeights::quantize_fp8
+ * quantizes a layer's seven projections (crates/reng-model/src/lib.rs:1882-1937):
+ * each matrix gets exactly what reng_hip_quantize would give it (HW chooses a
+ * bias per matrix), in as few launches as the shapes allow. mats is a host
+ * array of n descriptors (any n >= 1). */
+RENG_HIP_API int reng_hip_quantize_batch(const reng_hip_matrix *mats, size_t n, int dtype,
+                                         int format, int scaling, float backoff, void *stream);
+
+/* reng_fp8::row_absmax (lib.rs:439-458): per-row max |w|, NaN ignored, inf counted. */
+RENG_HIP_API int reng_hip_row_absmax(const void *w, int dtype, size_t rows, size_t cols, size_t ld,
+                                     float *out, void *stream);
+
+/* reng_fp8::choose_exp_bias (lib.rs:466-475), a host function. */
+RENG_HIP_API uint32_t reng_hip_choose_exp_bias(float absmax, int format);
+
+/* reng_fp8::encode over an array (lib.rs:154-201): f32 -> code, RNE, saturating,
+ * NaN -> sign | 0x7f. */
+RENG_HIP_API int reng_hip_encode(const float *x, size_t n, int format, uint8_t *codes, void *stream);
+
+/* reng_fp8::decode over an array (lib.rs:206-225): code -> f32 exactly; the top
+ * exponent field is +-inf (mantissa 0) or NaN. */
+RENG_HIP_API int reng_hip_decode(const uint8_t *codes, size_t n, int format, float *out, void *stream);
+
+/* Quantized::dequantize / dequantize_bf16 (lib.rs:328-344): out[r, c] =
+ * decode(codes[r, c]) * scales[r] as f32, or that rounded to bf16 (RNE). */
+RENG_HIP_API int reng_hip_dequantize(const uint8_t *codes, const float *scales, size_t rows,
+                                     size_t cols, int format, int out_dtype, void *out, void *stream);
+
+/* reng_fp8::row_errors (max_rows == 0) and sample_row_errors (max_rows > 0)
+ * (lib.rs:364-431): mean (f64 sum) and max of |dequant - w| / |w| over the
+ * non-zero weights of each (sampled) row; rows sampled every ceil(rows / n),
+ * n = min(max_rows, rows). mean_rel and max_rel hold one entry per sampled row. */
+RENG_HIP_API int reng_hip_row_errors(const uint16_t *w, const uint8_t *codes, const float *scales,
+                                     size_t rows, size_t cols, int format, size_t max_rows,
+                                     float *mean_rel, float *max_rel, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Consumer: fused fp8-dequant GEMV / GEMM
+ * ------------------------------------------------------------------------- */
+
+/* y[M, N] (bf16, RNE) = x[M, K] (bf16) . (decode(codes[N, K]) * scales[N])^T,
+ * f32 accumulation. This is the per-output-channel form of the reference's
+ * `fp8_gemm_bf16` complex guid (crates/reng-synapse/src/fp8.rs:278-331) with
+ * the bf16 activation the engine wants (the mixed pair gemm_mixed records as
+ * refused on Gaudi, fp8.rs:244-276); the CPU semantics are gemm_cpu over
+ * Quantized::dequantize (crates/reng-model/src/bin/fp8_probe.rs:55-67).
+ * Shapes are row-major: x [M, K], codes [N, K], y [M, N] (the reference's
+ * device sizes A [K, m], W [K, N] with transpose_b, out [N, m]).
+ * Batches 1..64 use in-register fp8 decode (GEMV for M <= 4, bf16 MFMA
+ * above); any M is accepted. scales may be NULL (unit scale, the 2-input form).
+ * Codes are the quantizer's finite codes; codes of the reserved top exponent
+ * field are read as OCP values, not as +-inf/NaN. K must be a multiple of 16. */
+RENG_HIP_API int reng_hip_gemm_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales,
+                                     size_t M, size_t N, size_t K, int format, uint16_t *y,
+                                     void *stream);
+
+/* gemm_fp8_scaled (crates/reng-synapse/src/fp8.rs:295-331): two fp8 operands
+ * and optional f32 scale operands, bf16 out on fp8 MFMA:
+ *   out[M, N] = sum_k decode(a[M, k]) * sa[m] * decode(b[N, k]) * sb[n]
+ * a [M, K] codes (the activation, e.g. from reng_hip_quantize with PCS over
+ * its rows, or UNIT as the reference's probe casts it, fp8_probe.rs:244-247),
+ * b [N, K] codes (the weight). scale_a has n_scale_a in {0 (unit), 1, M}
+ * entries, scale_b n_scale_b in {0, 1, N}. Both operands must be E4M3 or E5M2
+ * finite codes; K must be a multiple of 128. */
+RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const float *scale_a,
+                                          size_t n_scale_a, const uint8_t *b, int b_format,
+                                          const float *scale_b, size_t n_scale_b, size_t M,
+                                          size_t N, size_t K, uint16_t *out, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Self-check (no counterpart in the reference)
+ * ------------------------------------------------------------------------- */
+
+/* Runs every f32 bit pattern whose magnitude is at most the format's largest
+ * finite value through the hardware conversion the quantizer's fast path uses
+ * (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32) and through the exact integer
+ * encoder, and counts disagreements. The fast path is only valid on a device
+ * where this returns *mismatches == 0; tests/test_gpu_quantize.py requires it.
+ * Synchronous. first_mismatch receives the first disagreeing bit pattern. */
+RENG_HIP_API int reng_hip_verify_hw_convert(int format, uint64_t *mismatches,
+                                            uint32_t *first_mismatch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RENG_HIP_H */

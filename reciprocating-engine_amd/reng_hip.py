@@ -1,0 +1,306 @@
+"""Python binding of libreng_hip.so (include/reng_hip.h) over ctypes.
+
+The names follow the reference's reng-fp8 API (crates/reng-fp8/src/lib.rs):
+`quantize_with`, `quantize`, `encode`, `decode`, `row_absmax`, `row_errors`,
+`sample_row_errors`, `choose_exp_bias`, `Quantized.dequantize`, and the
+consumer `gemm_w8a16` / `gemm_fp8_scaled` (crates/reng-synapse/src/fp8.rs).
+
+Device work takes torch tensors that live on the GPU (torch is only the
+allocator and the stream here) and runs on torch's current stream. There is no
+CPU path: if the library is missing or a call fails, this module raises.
+Argument errors that reng-fp8 turns into panics (lib.rs:527-532) raise
+`ValueError` with the library's message.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libreng_hip.so")
+
+OK, EINVAL, EDEVICE, ENOMEM, EUNSUPPORTED = 0, 1, 2, 3, 4
+E4M3, E5M2 = 0, 1
+PCS, HW, UNIT = 0, 1, 2
+BF16, F32 = 0, 1
+DEFAULT_BACKOFF = 1.0
+
+FORMAT_NAMES = {"e4m3": E4M3, "fp8_143": E4M3, "hf8": E4M3, "e5m2": E5M2, "fp8_152": E5M2, "f8": E5M2}
+SCALING_NAMES = {"pcs": PCS, "per-channel": PCS, "perchannel": PCS, "hw": HW, "hw-exp-bias": HW,
+                 "expbias": HW, "unit": UNIT, "none": UNIT}
+MAX_FINITE = {E4M3: 240.0, E5M2: 57344.0}
+EXPONENT_BIAS = {E4M3: 7, E5M2: 15}
+
+
+class RengHipError(RuntimeError):
+    pass
+
+
+class _Matrix(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("exp_bias", ctypes.c_void_p), ("rows", ctypes.c_size_t), ("cols", ctypes.c_size_t),
+                ("ld", ctypes.c_size_t)]
+
+
+_lib = None
+_P, _SZ, _I, _F, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_uint32
+
+SIGNATURES = {
+    "reng_hip_version": (ctypes.c_char_p, []),
+    "reng_hip_last_error": (ctypes.c_char_p, []),
+    "reng_hip_device_info": (_I, [ctypes.c_char_p, _SZ]),
+    "reng_hip_quantize": (_I, [_P, _I, _SZ, _SZ, _SZ, _I, _I, _F, _P, _P, _P, _P]),
+    "reng_hip_quantize_host": (_I, [_P, _I, _SZ, _SZ, _I, _I, _F, _P, _P, _P]),
+    "reng_hip_quantize_batch": (_I, [ctypes.POINTER(_Matrix), _SZ, _I, _I, _I, _F, _P]),
+    "reng_hip_row_absmax": (_I, [_P, _I, _SZ, _SZ, _SZ, _P, _P]),
+    "reng_hip_choose_exp_bias": (_U32, [_F, _I]),
+    "reng_hip_encode": (_I, [_P, _SZ, _I, _P, _P]),
+    "reng_hip_decode": (_I, [_P, _SZ, _I, _P, _P]),
+    "reng_hip_dequantize": (_I, [_P, _P, _SZ, _SZ, _I, _I, _P, _P]),
+    "reng_hip_row_errors": (_I, [_P, _P, _P, _SZ, _SZ, _I, _SZ, _P, _P, _P]),
+    "reng_hip_gemm_w8a16": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _I, _P, _P]),
+    "reng_hip_gemm_fp8_scaled": (_I, [_P, _I, _P, _SZ, _P, _I, _P, _SZ, _SZ, _SZ, _SZ, _P, _P]),
+    "reng_hip_verify_hw_convert": (_I, [_I, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32)]),
+}
+
+
+def lib():
+    """Load libreng_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RengHipError(f"{LIB_PATH} is missing: build it with `make -C reciprocating-engine_amd`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != OK:
+        msg = lib().reng_hip_last_error().decode()
+        if rc == EINVAL:
+            raise ValueError(msg)
+        raise RengHipError(f"status {rc}: {msg}")
+
+
+def _fmt(f):
+    if isinstance(f, str):
+        if f.strip().lower() not in FORMAT_NAMES:
+            raise ValueError(f"unknown format {f}")
+        return FORMAT_NAMES[f.strip().lower()]
+    return int(f)
+
+
+def _sc(s):
+    if isinstance(s, str):
+        if s.strip().lower() not in SCALING_NAMES:
+            raise ValueError(f"unknown scaling {s}")
+        return SCALING_NAMES[s.strip().lower()]
+    return int(s)
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t, what):
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _dtype_code(t):
+    import torch
+
+    if t.dtype in (torch.bfloat16, torch.int16, torch.uint16):
+        return BF16
+    if t.dtype == torch.float32:
+        return F32
+    raise ValueError(f"weights must be bf16 (or its bits as int16/uint16) or f32, not {t.dtype}")
+
+
+def version():
+    return lib().reng_hip_version().decode()
+
+
+def device_info():
+    buf = ctypes.create_string_buffer(512)
+    _check(lib().reng_hip_device_info(buf, 512))
+    return buf.value.decode()
+
+
+def choose_exp_bias(absmax, fmt):
+    return int(lib().reng_hip_choose_exp_bias(float(absmax), _fmt(fmt)))
+
+
+class Quantized:
+    """reng_fp8::Quantized (lib.rs:291-345), holding device tensors."""
+
+    def __init__(self, format, scaling, rows, cols, codes, scales, exp_bias):
+        self.format, self.scaling = format, scaling
+        self.rows, self.cols = rows, cols
+        self.codes, self.scales = codes, scales
+        self.exp_bias = exp_bias
+
+    def code_bytes(self):
+        return self.rows * self.cols
+
+    def scale_operand(self):
+        return self.scales if _sc(self.scaling) == PCS else None
+
+    def dequantize(self):
+        import torch
+
+        out = torch.empty(self.rows * self.cols, dtype=torch.float32, device=self.codes.device)
+        _check(lib().reng_hip_dequantize(_dev(self.codes, "codes"), _dev(self.scales, "scales"), self.rows,
+                                         self.cols, _fmt(self.format), F32, _dev(out, "out"), _stream()))
+        return out
+
+    def dequantize_bf16(self):
+        import torch
+
+        out = torch.empty(self.rows * self.cols, dtype=torch.int16, device=self.codes.device)
+        _check(lib().reng_hip_dequantize(_dev(self.codes, "codes"), _dev(self.scales, "scales"), self.rows,
+                                         self.cols, _fmt(self.format), BF16, _dev(out, "out"), _stream()))
+        return out
+
+
+def quantize_into(w, rows, cols, fmt, scaling, backoff, codes, scales, exp_bias=None, ld=None):
+    """Device quantize into caller-owned tensors (no allocation)."""
+    _check(lib().reng_hip_quantize(_dev(w, "w"), _dtype_code(w), rows, cols, cols if ld is None else ld,
+                                   _fmt(fmt), _sc(scaling), float(backoff), _dev(codes, "codes"),
+                                   _dev(scales, "scales"),
+                                   None if exp_bias is None else _dev(exp_bias, "exp_bias"), _stream()))
+
+
+def quantize_with(w, rows, cols, fmt, scaling, backoff=DEFAULT_BACKOFF, ld=None):
+    """reng_fp8::quantize_with (lib.rs:519-563) on the GPU: w is a device tensor
+    of bf16 (or its int16 bits) or f32, [rows, ld] row-major."""
+    import torch
+
+    codes = torch.empty(rows * cols, dtype=torch.uint8, device=w.device)
+    scales = torch.empty(rows, dtype=torch.float32, device=w.device)
+    eb = torch.empty(1, dtype=torch.int32, device=w.device)
+    quantize_into(w, rows, cols, fmt, scaling, backoff, codes, scales, eb, ld)
+    return Quantized(fmt, scaling, rows, cols, codes, scales, int(eb.item()))
+
+
+def quantize(w, rows, cols, fmt, scaling):
+    return quantize_with(w, rows, cols, fmt, scaling, DEFAULT_BACKOFF)
+
+
+def quantize_host(w, rows, cols, fmt, scaling, backoff=DEFAULT_BACKOFF):
+    """The host-pointer entry (numpy in, numpy out), as Rust's quantize_with calls it."""
+    import numpy as np
+
+    w = np.ascontiguousarray(w)
+    dt = BF16 if w.dtype == np.uint16 else F32 if w.dtype == np.float32 else None
+    if dt is None:
+        raise ValueError(f"weights must be uint16 (bf16 bits) or float32, not {w.dtype}")
+    codes = np.empty(rows * cols, dtype=np.uint8)
+    scales = np.empty(rows, dtype=np.float32)
+    eb = ctypes.c_uint32(0)
+    _check(lib().reng_hip_quantize_host(ctypes.c_void_p(w.ctypes.data), dt, rows, cols, _fmt(fmt), _sc(scaling),
+                                        float(backoff), ctypes.c_void_p(codes.ctypes.data),
+                                        ctypes.c_void_p(scales.ctypes.data), ctypes.byref(eb)))
+    return codes, scales, int(eb.value)
+
+
+def quantize_batch(mats, fmt, scaling, backoff=DEFAULT_BACKOFF, dtype=BF16):
+    """mats: list of (w, rows, cols, codes, scales, exp_bias_or_None) device tensors."""
+    arr = (_Matrix * len(mats))()
+    for i, (w, rows, cols, codes, scales, eb) in enumerate(mats):
+        arr[i] = _Matrix(w.data_ptr(), codes.data_ptr(), scales.data_ptr(),
+                         0 if eb is None else eb.data_ptr(), rows, cols, cols)
+    _check(lib().reng_hip_quantize_batch(arr, len(mats), dtype, _fmt(fmt), _sc(scaling), float(backoff),
+                                         _stream()))
+
+
+def row_absmax(w, rows, cols, ld=None):
+    import torch
+
+    out = torch.empty(rows, dtype=torch.float32, device=w.device)
+    _check(lib().reng_hip_row_absmax(_dev(w, "w"), _dtype_code(w), rows, cols, cols if ld is None else ld,
+                                     _dev(out, "out"), _stream()))
+    return out
+
+
+def encode(x, fmt):
+    """encode over a device f32 tensor -> uint8 codes."""
+    import torch
+
+    out = torch.empty(x.numel(), dtype=torch.uint8, device=x.device)
+    _check(lib().reng_hip_encode(_dev(x, "x"), x.numel(), _fmt(fmt), _dev(out, "out"), _stream()))
+    return out
+
+
+def decode(codes, fmt):
+    import torch
+
+    out = torch.empty(codes.numel(), dtype=torch.float32, device=codes.device)
+    _check(lib().reng_hip_decode(_dev(codes, "codes"), codes.numel(), _fmt(fmt), _dev(out, "out"), _stream()))
+    return out
+
+
+def _errors(w, q, max_rows):
+    import torch
+
+    n = q.rows if max_rows == 0 else min(max_rows, q.rows)
+    step = -(-q.rows // n)
+    k = -(-q.rows // step)
+    mean = torch.empty(k, dtype=torch.float32, device=q.codes.device)
+    mx = torch.empty(k, dtype=torch.float32, device=q.codes.device)
+    _check(lib().reng_hip_row_errors(_dev(w, "w"), _dev(q.codes, "codes"), _dev(q.scales, "scales"), q.rows,
+                                     q.cols, _fmt(q.format), max_rows, _dev(mean, "mean"), _dev(mx, "max"),
+                                     _stream()))
+    return mean, mx
+
+
+def row_errors(w, q):
+    return _errors(w, q, 0)
+
+
+def sample_row_errors(w, q, max_rows):
+    if max_rows == 0:
+        raise ValueError("max_rows must be positive")
+    return _errors(w, q, max_rows)
+
+
+def gemm_w8a16(x, codes, scales, M, N, K, fmt, y=None):
+    """y[M, N] bf16 = x[M, K] bf16 . (decode(codes[N, K]) * scales[N])^T."""
+    import torch
+
+    if y is None:
+        y = torch.empty(M * N, dtype=torch.bfloat16, device=x.device)
+    _check(lib().reng_hip_gemm_w8a16(_dev(x, "x"), _dev(codes, "codes"),
+                                     None if scales is None else _dev(scales, "scales"), M, N, K, _fmt(fmt),
+                                     _dev(y, "y"), _stream()))
+    return y
+
+
+def gemm_fp8_scaled(a, a_fmt, scale_a, b, b_fmt, scale_b, M, N, K, out=None):
+    """gemm_fp8_scaled (crates/reng-synapse/src/fp8.rs:295-331): bf16 out[M, N]."""
+    import torch
+
+    if out is None:
+        out = torch.empty(M * N, dtype=torch.bfloat16, device=a.device)
+    na = 0 if scale_a is None else scale_a.numel()
+    nb = 0 if scale_b is None else scale_b.numel()
+    _check(lib().reng_hip_gemm_fp8_scaled(_dev(a, "a"), _fmt(a_fmt), None if scale_a is None else _dev(scale_a, "sa"),
+                                          na, _dev(b, "b"), _fmt(b_fmt),
+                                          None if scale_b is None else _dev(scale_b, "sb"), nb, M, N, K,
+                                          _dev(out, "out"), _stream()))
+    return out
+
+
+def verify_hw_convert(fmt):
+    n = ctypes.c_uint64(0)
+    first = ctypes.c_uint32(0)
+    _check(lib().reng_hip_verify_hw_convert(_fmt(fmt), ctypes.byref(n), ctypes.byref(first)))
+    return int(n.value), int(first.value)

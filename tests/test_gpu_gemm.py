@@ -1,0 +1,194 @@
+"""The fused fp8-dequant GEMV / skinny GEMM and the fp8 x fp8 GEMM against the
+oracle's f32 gemm_cpu over Quantized::dequantize (fp8_probe.rs:55-78).
+
+Tolerance: relative L2 < 1e-2 over the bf16 outputs (
+the reference probe's own acceptance is 0.02, fp8_probe.rs:327,344). For the
+fp8 x fp8 path the reference product uses the dequantized fp8 activation, as
+the reference probe does (fp8_probe.rs:242-248, 295-298). Exactness of the
+in-register decode is checked on its own: a one-hot activation reads every
+finite code back bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import E4M3, E5M2, bf16_bits, bf16_f32, probe_activations, probe_weights
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def R():
+    import reng_hip
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    reng_hip.lib()
+    return reng_hip
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def bf16_out(t):
+    return bf16_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def quantized_weight(rng, n, k, fmt, sigma=0.02):
+    w = bf16_bits((rng.standard_normal((n, k)) * sigma).astype(np.float32)).ravel()
+    return O.quantize(w, n, k, fmt, "pcs")
+
+
+def check_w8a16(R, rng, M, N, K, fmt, sample_cols=None):
+    q = quantized_weight(rng, N, K, fmt)
+    x = bf16_bits(rng.standard_normal((M, K)).astype(np.float32)).ravel()
+    y = bf16_out(R.gemm_w8a16(dev(x), dev(q.codes), dev(q.scales), M, N, K, fmt)).reshape(M, N)
+    deq = q.dequantize()
+    if sample_cols is None:
+        want = O.gemm(bf16_f32(x), deq, M, K, N, threads=16).reshape(M, N)
+        got = y
+    else:
+        idx = np.unique(np.concatenate([rng.choice(N, sample_cols, replace=False), [0, N - 1]]))
+        want = O.gemm_cols(bf16_f32(x), deq, M, K, idx, threads=16).reshape(M, idx.size)
+        got = y[:, idx]
+    rel = O.rel_l2(got.ravel(), want.ravel())
+    assert rel < TOL, f"M={M} N={N} K={K} fmt={fmt}: rel_L2 {rel}"
+    assert np.all(np.isfinite(y))
+    return rel
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_in_register_decode_reads_every_finite_code_exactly(R, fmt):
+    """Row n of the weight is code n (all finite codes), the activation is one-hot
+    at k, so y[m, n] = decode(code) * s exactly (bf16 holds every fp8 value)."""
+    maxc = 0x77 if fmt == E4M3 else 0x7B
+    codes = np.array([c for c in range(256) if (c & 0x7F) <= maxc], dtype=np.uint8)
+    N, K = codes.size, 64
+    w = np.zeros((N, K), dtype=np.uint8)
+    for kk in range(K):
+        w[:, kk] = np.roll(codes, kk)
+    scales = np.ones(N, dtype=np.float32)
+    for M in (1, 4, 16):
+        x = np.zeros((M, K), dtype=np.uint16)
+        for m in range(M):
+            x[m, (5 * m + 3) % K] = 0x3F80   # 1.0
+        y = bf16_out(R.gemm_w8a16(dev(x.ravel()), dev(w.ravel()), dev(scales), M, N, K, fmt)).reshape(M, N)
+        for m in range(M):
+            kk = (5 * m + 3) % K
+            want = O.decode_array(w[:, kk], fmt)
+            # A sum of products cannot return -0.0 (-0 + 0 = +0), so compare values;
+            # every non-zero value must match bit for bit.
+            assert np.array_equal(y[m], want), (M, m)
+            nz = want != 0
+            assert np.array_equal(y[m][nz].view(np.uint32), want[nz].view(np.uint32)), (M, m)
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336)])
+def test_gemv_batch1_llama_8b_shapes(R, fmt, shape):
+    rng = np.random.default_rng(101 + fmt)
+    N, K = shape
+    check_w8a16(R, rng, 1, N, K, fmt)
+
+
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_gemv_small_batches(R, M):
+    rng = np.random.default_rng(103 + M)
+    check_w8a16(R, rng, M, 1024, 4096, E4M3)
+    check_w8a16(R, rng, M, 100, 176, E5M2)
+
+
+QWEN_7B = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]
+
+
+@pytest.mark.parametrize("M", [8, 64])
+@pytest.mark.parametrize("shape", QWEN_7B)
+def test_skinny_gemm_qwen_7b_shapes(R, M, shape):
+    rng = np.random.default_rng(107 + M)
+    N, K = shape
+    check_w8a16(R, rng, M, N, K, E4M3, sample_cols=512)
+
+
+@pytest.mark.parametrize("M", [5, 16, 17, 33, 65, 130])
+def test_skinny_gemm_ragged_batches(R, M):
+    rng = np.random.default_rng(109 + M)
+    check_w8a16(R, rng, M, 200, 512, E4M3)
+    check_w8a16(R, rng, M, 48, 4096, E5M2)
+
+
+def test_the_reference_probe_shapes(R):
+    """fp8_probe.rs:478-505: weights(512, 256), m in {1, 256}, rel_L2 < 0.02."""
+    N, K = 512, 256
+    w = probe_weights(N, K)
+    q = O.quantize(w, N, K, E4M3, "pcs")
+    for m in (1, 256):
+        a = bf16_bits(probe_activations(m * K))
+        y = bf16_out(R.gemm_w8a16(dev(a), dev(q.codes), dev(q.scales), m, N, K, E4M3))
+        want = O.gemm(bf16_f32(a), q.dequantize(), m, K, N)
+        assert O.rel_l2(y, want) < TOL
+        # The 2-input form: no scale operand, the product over the raw codes.
+        y2 = bf16_out(R.gemm_w8a16(dev(a), dev(q.codes), None, m, N, K, E4M3))
+        raw = O.decode_array(q.codes, E4M3)
+        assert O.rel_l2(y2, O.gemm(bf16_f32(a), raw, m, K, N)) < TOL
+
+
+def test_w8a16_refuses_bad_shapes(R):
+    x = torch.zeros(64, dtype=torch.int16, device="cuda")
+    c = torch.zeros(64 * 8, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError, match="multiple of 16"):
+        R.gemm_w8a16(x, c, None, 1, 8, 40, E4M3)
+    with pytest.raises(ValueError, match="empty product"):
+        R.gemm_w8a16(x, c, None, 0, 8, 64, E4M3)
+
+
+# ------------------------------------------------------------ fp8 x fp8
+
+
+def check_fp8(R, rng, M, N, K, fa, fb, act="pcs", nsb="N", sample_cols=None):
+    x = bf16_bits(rng.standard_normal((M, K)).astype(np.float32)).ravel()
+    qa = O.quantize(x, M, K, fa, act)
+    qw = quantized_weight(rng, N, K, fb)
+    sa = None if act == "unit" else qa.scales
+    sb = {"N": qw.scales, "1": qw.scales[:1].copy(), "0": None}[nsb]
+    out = bf16_out(R.gemm_fp8_scaled(dev(qa.codes), fa, None if sa is None else dev(sa), dev(qw.codes), fb,
+                                     None if sb is None else dev(sb), M, N, K)).reshape(M, N)
+    a_deq = qa.dequantize()
+    if sb is None:
+        b_scale = np.float32(1.0)
+    elif sb.size == 1:
+        b_scale = sb[0]
+    else:
+        b_scale = np.repeat(sb, K)
+    b_deq = (O.decode_array(qw.codes, fb) * b_scale).astype(np.float32)
+    if sample_cols:
+        idx = np.unique(np.concatenate([rng.choice(N, sample_cols, replace=False), [0, N - 1]]))
+        want = O.gemm_cols(a_deq, b_deq, M, K, idx, threads=16).reshape(M, idx.size)
+        got = out[:, idx]
+    else:
+        want = O.gemm(a_deq, b_deq, M, K, N, threads=16).reshape(M, N)
+        got = out
+    rel = O.rel_l2(got.ravel(), want.ravel())
+    assert rel < TOL, f"M={M} N={N} K={K} {fa}x{fb} act={act} sb={nsb}: rel_L2 {rel}"
+    return rel
+
+
+@pytest.mark.parametrize("fa,fb", [(E4M3, E4M3), (E5M2, E5M2), (E4M3, E5M2), (E5M2, E4M3)])
+def test_fp8_gemm_formats_and_scale_forms(R, fa, fb):
+    rng = np.random.default_rng(113 + 2 * fa + fb)
+    for act, nsb in (("pcs", "N"), ("unit", "N"), ("pcs", "1"), ("unit", "0")):
+        check_fp8(R, rng, 160, 200, 384, fa, fb, act, nsb)
+
+
+@pytest.mark.parametrize("shape", [(5120, 5120), (1024, 5120), (27648, 5120), (5120, 27648)])
+def test_fp8_gemm_prefill_qwen_32b_shapes(R, shape):
+    rng = np.random.default_rng(127)
+    N, K = shape
+    check_fp8(R, rng, 1024, N, K, E4M3, E4M3, sample_cols=192)
