@@ -1,0 +1,391 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fp8 weight quantizer and its fused dequant GEMV / GEMM.
+
+Headline (one JSON line on stdout): quantize throughput in GB/s of algorithmic
+bytes over the full Llama-3.1-8B-shaped bf16 weight set (32 layers of
+q/o [4096, 4096], k/v [1024, 4096], gate/up [14336, 4096], down [4096, 14336];
+6,979,321,856 elements; N(0, 0.02) with all-zero rows, bf16 subnormals and
+out-of-range values injected), E4M3, per-output-channel absmax scales,
+backoff 1. One step = one pass of the quantizer over the whole set, inputs
+already resident in HBM. Algorithmic bytes per element: 2 (bf16 in) + 1 (code
+out), plus 4 per row (f32 scale).
+
+Also reported (under "extras"): E5M2 over the same set; the f32 [2048, 2048]
+quantize rotated over 32 copies; the fused dequant GEMV at batch 1 on the
+[14336, 4096] and [4096, 14336] shapes rotated over 32 layers; the skinny GEMM at
+batch 8 and 64 on Qwen2.5-7B shapes; the M = 1024 fp8 x fp8 GEMM on
+Qwen2.5-32B shapes. With --extended, the full Qwen2.5-32B quantize.
+
+The CPU baseline is the oracle (a C restatement of reng-fp8's quantizer: two
+passes, an IEEE divide per element, <= 8 threads by reng-fp8's split rule)
+timed on this host over layers 0-7 of the same set; those layers are also
+compared bit for bit with the GPU's codes and scales.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--extended]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "reciprocating-engine_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+METRIC = "quantize GB/s; fp8 GEMV/GEMM % HBM/MFMA roofline, 8B shapes b1-b64"
+HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
+FP8_PEAK = 5.0e15            # MI355X dense fp8 MFMA, flop/s
+MALL_BYTES = 256 << 20       # Infinity Cache: timed buffers rotate over more than this
+
+LLAMA_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+            ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+QWEN_7B = [("q/o", 3584, 3584), ("k/v", 512, 3584), ("gate/up", 18944, 3584), ("down", 3584, 18944)]
+QWEN_32B = [("q", 5120, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120, 5120),
+            ("gate", 27648, 5120), ("up", 27648, 5120), ("down", 5120, 27648)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def quant_bytes(rows, cols, in_bytes=2):
+    return rows * cols * (in_bytes + 1) + 4 * rows
+
+
+def make_bf16(torch, rows, cols, gen, inject=True):
+    """N(0, 0.02) bf16 bits (int16 view) with the workload's injections."""
+    w = (torch.randn(rows, cols, device="cuda", generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16)
+    if inject:
+        nz = max(1, rows // 1000)                      # all-zero rows, 0.1%
+        w[torch.randint(0, rows, (nz,), device="cuda", generator=gen)] = 0
+        flat = w.view(-1)
+        n = flat.numel()
+        ns = max(1, n // 10000)                        # bf16 subnormals, 0.01%
+        idx = torch.randint(0, n, (ns,), device="cuda", generator=gen)
+        sub = torch.randint(1, 0x80, (ns,), device="cuda", generator=gen, dtype=torch.int32)
+        sign = torch.randint(0, 2, (ns,), device="cuda", generator=gen, dtype=torch.int32) << 15
+        flat[idx] = (sub | sign).to(torch.int32).to(torch.int16)
+        nb = max(1, n // 1000000)                      # out-of-range finite values, 1 ppm
+        idx = torch.randint(0, n, (nb,), device="cuda", generator=gen)
+        vals = torch.tensor([1e4, -1e4, 3e38, -3e38], device="cuda").to(torch.bfloat16).view(torch.int16)
+        flat[idx] = vals[torch.randint(0, 4, (nb,), device="cuda", generator=gen)]
+    return w.view(-1)
+
+
+class WeightSet:
+    def __init__(self, torch, shapes, layers, seed):
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(seed)
+        self.mats = []   # (layer, name, rows, cols, w, codes, scales, exp_bias)
+        for layer in range(layers):
+            for name, rows, cols in shapes:
+                w = make_bf16(torch, rows, cols, gen)
+                codes = torch.empty(rows * cols, dtype=torch.uint8, device="cuda")
+                scales = torch.empty(rows, dtype=torch.float32, device="cuda")
+                eb = torch.zeros(1, dtype=torch.int32, device="cuda")
+                self.mats.append((layer, name, rows, cols, w, codes, scales, eb))
+        self.elements = sum(m[2] * m[3] for m in self.mats)
+        self.bytes = sum(quant_bytes(m[2], m[3]) for m in self.mats)
+
+    def launches(self):
+        """The set as the library launches it: matrices grouped by row width,
+        32 per launch (the batch descriptors travel in the kernel arguments)."""
+        by_cols = {}
+        for m in self.mats:
+            by_cols.setdefault(m[3], []).append(m)
+        out = []
+        for cols in sorted(by_cols):
+            ms = by_cols[cols]
+            for i in range(0, len(ms), 32):
+                chunk = ms[i:i + 32]
+                out.append((cols, chunk, sum(quant_bytes(m[2], m[3]) for m in chunk)))
+        return out
+
+
+def time_quantize(torch, R, ws, fmt, steps, warmup):
+    launches = ws.launches()
+    batches = [[(m[4], m[2], m[3], m[5], m[6], m[7]) for m in chunk] for _, chunk, _ in launches]
+
+    def step(evs=None):
+        for i, b in enumerate(batches):
+            if evs is not None:
+                evs[i][0].record()
+            R.quantize_batch(b, fmt, "pcs", 1.0)
+            if evs is not None:
+                evs[i][1].record()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in batches]
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        step(evs[s])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch = [[a.elapsed_time(b) * 1e-3 for a, b in e] for e in evs]
+    step_s = wall / steps
+    # The dominant kernel: the configuration carrying the most bytes per step.
+    by_cfg = {}
+    for i, (cols, _, nbytes) in enumerate(launches):
+        d = by_cfg.setdefault(cols, {"bytes": 0, "secs": 0.0, "launches": 0})
+        d["bytes"] += nbytes * steps
+        d["secs"] += sum(per_launch[s][i] for s in range(steps))
+        d["launches"] += steps
+    dom_cols = max(by_cfg, key=lambda c: by_cfg[c]["bytes"])
+    d = by_cfg[dom_cols]
+    return {
+        "step_s": step_s,
+        "gbps": ws.bytes / step_s / 1e9,
+        "kernel_sum_s": sum(sum(p) for p in per_launch) / steps,
+        "dominant": {"cols": dom_cols, "bytes_per_launch": d["bytes"] / d["launches"],
+                     "secs_per_launch": d["secs"] / d["launches"], "launches_per_step": d["launches"] // steps},
+        "configs": {str(c): {"GBps": v["bytes"] / v["secs"] / 1e9, "launches_per_step": v["launches"] // steps}
+                    for c, v in by_cfg.items()},
+    }
+
+
+def cpu_baseline_and_parity(torch, O, ws, fmt, layers=8):
+    import numpy as np
+
+    sample = [m for m in ws.mats if m[0] < layers]
+    host = [(m[2], m[3], m[4].cpu().numpy().view(np.uint16)) for m in sample]
+    elems = sum(r * c for r, c, _ in host)
+    nbytes = sum(quant_bytes(r, c) for r, c, _ in host)
+    t0 = time.perf_counter()
+    refs = [O.quantize_with(w, r, c, fmt, "pcs", 1.0, thread_cap=8) for r, c, w in host]
+    secs = time.perf_counter() - t0
+    mismatched = 0
+    for m, ref in zip(sample, refs):
+        if not (np.array_equal(m[5].cpu().numpy(), ref.codes)
+                and np.array_equal(m[6].cpu().numpy().view(np.uint32), ref.scales.view(np.uint32))
+                and int(m[7].item()) == ref.exp_bias):
+            mismatched += 1
+    model = "unknown CPU"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    threads = max(O.split(r, c) for r, c, _ in host)
+    return ({"value": round(nbytes / secs / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+             "sample": (f"layers 0-{layers - 1} of the same set ({len(sample)} matrices, {elems} elements, "
+                        f"{secs:.1f} s), the oracle's C restatement of reng-fp8 quantize_with run matrix by "
+                        f"matrix with reng-fp8's split rule (<= 8 threads), {model}, nproc {os.cpu_count()}")},
+            {"matrices": len(sample), "mismatched": mismatched})
+
+
+def graph_time(torch, fn, n_launch, reps=3):
+    """Mean seconds per launch of fn(i) for i in 0..n_launch-1 replayed from a hipGraph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(n_launch):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_launch):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        t = a.elapsed_time(b) * 1e-3 / n_launch
+        best = t if best is None else min(best, t)
+    return best
+
+
+def rotation(nbytes, floor=4, cap=1024):
+    n = max(floor, -(-2 * MALL_BYTES // max(1, nbytes)))
+    return min(cap, n)
+
+
+def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3"):
+    per = N * K
+    copies = rotation(per)
+    ws = []
+    for _ in range(copies):
+        w = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16).view(-1)
+        q = R.quantize_with(w, N, K, fmt, "pcs")
+        ws.append((q.codes, q.scales))
+        del w
+    x = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16).view(-1)
+    y = torch.empty(M * N, dtype=torch.bfloat16, device="cuda")
+    secs = graph_time(torch, lambda i: R.gemm_w8a16(x, ws[i % copies][0], ws[i % copies][1], M, N, K, fmt, y),
+                      max(2 * copies, 40))
+    nbytes = N * K + 4 * N + 2 * M * K + 2 * M * N
+    flops = 2 * M * N * K
+    return {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
+            "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "TFLOPs": round(flops / secs / 1e12, 2),
+            "rotated_copies": copies}
+
+
+def bench_fp8_gemm(torch, R, gen, M, N, K):
+    w = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16).view(-1)
+    qw = R.quantize_with(w, N, K, "e4m3", "pcs")
+    del w
+    x = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16).view(-1)
+    qa = R.quantize_with(x, M, K, "e4m3", "pcs")     # per-token activation scales
+    out = torch.empty(M * N, dtype=torch.bfloat16, device="cuda")
+    secs = graph_time(torch, lambda i: R.gemm_fp8_scaled(qa.codes, "e4m3", qa.scales, qw.codes, "e4m3",
+                                                         qw.scales, M, N, K, out), 10)
+    flops = 2 * M * N * K
+    return {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 1), "TFLOPs": round(flops / secs / 1e12, 1),
+            "mfma_frac": round(flops / secs / FP8_PEAK, 3)}
+
+
+def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048):
+    copies = 32
+    mats = []
+    for _ in range(copies):
+        x = torch.randn(rows, cols, device="cuda", generator=gen) * 0.02
+        out = torch.rand(rows, cols, device="cuda", generator=gen) < 0.001   # 0.1% outliers x50
+        x = torch.where(out, x * 50.0, x).contiguous().view(-1)
+        mats.append((x, torch.empty(rows * cols, dtype=torch.uint8, device="cuda"),
+                     torch.empty(rows, dtype=torch.float32, device="cuda")))
+    secs = graph_time(torch, lambda i: R.quantize_into(mats[i % copies][0], rows, cols, "e4m3", "pcs", 1.0,
+                                                       mats[i % copies][1], mats[i % copies][2]), 2 * copies)
+    nbytes = quant_bytes(rows, cols, 4)
+    return {"rows": rows, "cols": cols, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
+            "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "rotated_copies": copies}
+
+
+def read_traffic(kind):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC
+    summary (profiles/<kind>_traffic.txt: `fetch_bytes` and `write_bytes` lines,
+    already scaled by the copy-kernel calibration), or None."""
+    p = os.path.join(ROOT, "profiles", f"{kind}_traffic.txt")
+    try:
+        vals = {}
+        for line in open(p):
+            if ":" in line and not line.startswith("#"):
+                k, v = line.split(":", 1)
+                vals[k.strip()] = v.strip()
+        return int(float(vals["fetch_bytes"])) + int(float(vals["write_bytes"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--format", default="e4m3")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--extended", action="store_true", help="also the full Qwen2.5-32B quantize")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this path runs on a single MI355X and has no multi-GPU "
+              f"form here (asked for --gpus {args.gpus}, WORLD_SIZE {world}).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import reng_hip as R
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    R.lib()
+    log("device:", R.device_info())
+    t0 = time.perf_counter()
+    ws = WeightSet(torch, LLAMA_8B, 32, seed=1234)
+    torch.cuda.synchronize()
+    log(f"Llama-3.1-8B set: {len(ws.mats)} matrices, {ws.elements} elements, {ws.bytes / 1e9:.3f} GB "
+        f"algorithmic per pass, generated in {time.perf_counter() - t0:.1f} s")
+
+    set_elements, set_bytes = ws.elements, ws.bytes
+    res = time_quantize(torch, R, ws, args.format, args.steps, args.warmup)
+    log(f"quantize {args.format}: {res['step_s'] * 1e3:.3f} ms/step, {res['gbps']:.1f} GB/s, "
+        f"per config {res['configs']}")
+    dom = res["dominant"]
+    achieved = dom["bytes_per_launch"] / dom["secs_per_launch"] / 1e9
+    traffic = read_traffic("quantize")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic,
+                "kernel": f"quantize_rows_fast (bf16, {args.format}, rows of {dom['cols']})",
+                "algorithmic_bytes_per_launch": int(dom["bytes_per_launch"]),
+                "mean_launch_us": round(dom["secs_per_launch"] * 1e6, 1)}
+
+    cpu, parity = None, None
+    if not args.no_cpu:
+        import oracle as O
+
+        cpu, parity = cpu_baseline_and_parity(torch, O, ws, args.format)
+        log(f"cpu baseline {cpu['value']} GB/s; parity {parity}")
+
+    extras = {}
+    if not args.no_extras:
+        other = "e5m2" if args.format == "e4m3" else "e4m3"
+        r2 = time_quantize(torch, R, ws, other, max(3, args.steps // 4), 1)
+        extras[f"quantize_{other}_GBps"] = round(r2["gbps"], 1)
+        extras[f"quantize_{other}_ms_per_step"] = round(r2["step_s"] * 1e3, 3)
+        del ws
+        torch.cuda.empty_cache()
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(99)
+        extras["f32_2048x2048_quantize"] = bench_f32_quantize(torch, R, gen)
+        extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096),
+                                     bench_w8a16(torch, R, gen, 1, 4096, 14336)]
+        log("gemv b1:", extras["gemv_b1_llama8b"])
+        sk = []
+        for M in (8, 64):
+            for _, N, K in QWEN_7B:
+                sk.append(bench_w8a16(torch, R, gen, M, N, K))
+        extras["skinny_qwen7b"] = sk
+        log("skinny:", sk)
+        torch.cuda.empty_cache()
+        extras["prefill_fp8_m1024_qwen32b"] = [bench_fp8_gemm(torch, R, gen, 1024, N, K)
+                                               for N, K in ((5120, 5120), (1024, 5120), (27648, 5120),
+                                                            (5120, 27648))]
+        log("prefill fp8:", extras["prefill_fp8_m1024_qwen32b"])
+        torch.cuda.empty_cache()
+        if args.extended:
+            wq = WeightSet(torch, QWEN_32B, 64, seed=4321)
+            r3 = time_quantize(torch, R, wq, "e4m3", 3, 1)
+            extras["quantize_qwen32b_e4m3"] = {"elements": wq.elements, "ms_per_step": round(r3["step_s"] * 1e3, 2),
+                                               "GBps": round(r3["gbps"], 1)}
+            del wq
+
+    out = {
+        "metric": METRIC,
+        "value": round(res["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["step_s"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": ("Llama-3.1-8B-shaped bf16 weight set, 32 layers x (q/o [4096,4096], "
+                                "k/v [1024,4096], gate/up [14336,4096], down [4096,14336]), N(0,0.02) with "
+                                "0.1% zero rows, 0.01% bf16 subnormals, 1 ppm out-of-range values"),
+                   "elements": set_elements, "format": args.format, "scaling": "pcs", "backoff": 1.0,
+                   "algorithmic_bytes_per_step": set_bytes},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "parity": parity,
+        "extras": extras,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -167,12 +167,13 @@ RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const 
  * Self-check (no counterpart in the reference)
  * ------------------------------------------------------------------------- */
 
-/* Runs every f32 bit pattern whose magnitude is at most the format's largest
- * finite value through the hardware conversion the quantizer's fast path uses
- * (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32) and through the exact integer
- * encoder, and counts disagreements. The fast path is only valid on a device
- * where this returns *mismatches == 0; tests/test_gpu_quantize.py requires it.
- * Synchronous. first_mismatch receives the first disagreeing bit pattern. */
+/* Runs every non-NaN f32 bit pattern through the hardware conversion the
+ * quantizer's fast path uses (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32: after a
+ * clamp to +-max finite, and without the clamp below 248 / 61440) and through
+ * the exact integer encoder, and counts disagreements. The fast path is only
+ * valid on a device where this returns *mismatches == 0;
+ * tests/test_gpu_quantize.py requires it. Synchronous. first_mismatch
+ * receives the first disagreeing bit pattern. */
 RENG_HIP_API int reng_hip_verify_hw_convert(int format, uint64_t *mismatches,
                                             uint32_t *first_mismatch);
 

@@ -105,9 +105,12 @@ __global__ __launch_bounds__(256) void row_errors_kernel(const uint16_t *__restr
 }
 
 // Every non-NaN f32 pattern: the conversion as the fast path uses it (clamped
-// into +-max finite, then v_cvt_pk_*) against the exact integer encoder.
+// into +-max finite, then v_cvt_pk_*) against the exact integer encoder; and,
+// below the first midpoint past the largest finite value (248 / 61440), the
+// unclamped conversion too.
 template <int F>
 __global__ void verify_hw_kernel(unsigned long long *__restrict__ count, uint32_t *__restrict__ first) {
+    constexpr float UNCLAMPED = F == RENG_HIP_E4M3 ? 248.0f : 61440.0f;
     unsigned long long bad = 0;
     uint32_t fbad = 0xffffffffu;
     const uint64_t total = 1ull << 32;
@@ -116,9 +119,11 @@ __global__ void verify_hw_kernel(unsigned long long *__restrict__ count, uint32_
         const uint32_t u = (uint32_t)i;
         const float x = __uint_as_float(u);
         if (__builtin_isnan(x)) continue;
-        const uint32_t hw = cvt_pk_lo<F>(prep<F, true>(x), 0.0f, 0u) & 0xffu;
         const uint32_t ex = encode_exact<F>(x);
-        if (hw != ex) {
+        bool ok = (cvt_pk_lo<F>(prep<F, true>(x), 0.0f, 0u) & 0xffu) == ex;
+        // Unclamped, below the first midpoint past the largest finite value.
+        if (__builtin_fabsf(x) < UNCLAMPED) ok = ok && (cvt_pk_lo<F>(x, 0.0f, 0u) & 0xffu) == ex;
+        if (!ok) {
             ++bad;
             fbad = u < fbad ? u : fbad;
         }

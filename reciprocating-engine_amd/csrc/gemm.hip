@@ -61,51 +61,121 @@ __device__ __forceinline__ float bf_hi(uint32_t d) { return __uint_as_float(d & 
 
 // ------------------------------------------------------------------ GEMV
 
-// One wave per output row n (rows strided over the grid), lanes over K in
-// 16-code chunks. x is read through the caches (it is shared by every row).
-template <int F, int M>
-__global__ __launch_bounds__(256) void gemv_w8a16(const uint16_t *__restrict__ x,
+// v_dot2_f32_bf16: acc + a.lo * b.lo + a.hi * b.hi, f32 accumulation.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
+                                           acc, false);
+}
+
+// 16 codes (a 16-byte load) -> 8 bf16 pairs, exactly.
+template <int F>
+__device__ __forceinline__ void decode16(const u32x4 &q, uint32_t (&w)[8]) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w[2 * i] = __builtin_bit_cast(uint32_t, dec2_bf16<F>(d[i], false));
+        w[2 * i + 1] = __builtin_bit_cast(uint32_t, dec2_bf16<F>(d[i], true));
+    }
+}
+
+// One wave per output row (rows strided over all waves of the grid), 16 codes
+// per lane per chunk, CPL chunks per lane per group. The wave walks its
+// (row, group) pairs as one stream and loads the next pair before consuming
+// the current one, so CPL * 1 KB of codes per wave stay in flight through the
+// decode, the dot products and the end-of-row reduction. The activation rows
+// are staged once per block in LDS as bf16 (XLDS) or read through the caches.
+// Codes decode to bf16 pairs in registers and meet the activation in
+// v_dot2_f32_bf16 (f32 accumulation).
+template <int F, int M, int CPL, bool XLDS>
+__global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x,
                                                   const uint8_t *__restrict__ codes,
                                                   const float *__restrict__ scales, uint32_t N,
                                                   uint32_t K, uint16_t *__restrict__ y) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
-    const uint32_t kc = K / 16;   // 16-code chunks per row
-    for (uint32_t n = wave; n < N; n += nwaves) {
-        const u32x4 *wr = reinterpret_cast<const u32x4 *>(codes + (size_t)n * K);
-        float acc[M];
+    extern __shared__ __attribute__((aligned(16))) uint32_t xs[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t nch = K / 16;   // 16-code chunks per row
+    const uint32_t waves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (tid >> 6);
+    const uint32_t gpr = (nch + 64 * CPL - 1) / (64 * CPL);   // groups per row
+    const bool ragged = nch % (64 * CPL) != 0;
+
+    auto load = [&](uint32_t r, uint32_t gi, u32x4 (&q)[CPL]) {
+        const u32x4 *wr = reinterpret_cast<const u32x4 *>(codes + (size_t)r * K);
+        const uint32_t c0 = gi * 64 * CPL + lane;
 #pragma unroll
-        for (int m = 0; m < M; ++m) acc[m] = 0.0f;
-        for (uint32_t c = lane; c < kc; c += 64) {
-            const u32x4 q = __builtin_nontemporal_load(wr + c);
-            float w[16];
-            const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+        for (int u = 0; u < CPL; ++u) {
+            const uint32_t ch = c0 + u * 64;
+            q[u] = (!ragged || ch < nch) ? __builtin_nontemporal_load(wr + ch) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+
+    // The first group's codes are requested before the activation is staged.
+    uint32_t r = wave, gi = 0;
+    u32x4 qn[CPL];
+    if (wave < N) load(r, gi, qn);
+    if constexpr (XLDS) {
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(x);
+        u32x4 *dst = reinterpret_cast<u32x4 *>(xs);
+        for (uint32_t i = tid; i < M * nch * 2; i += blockDim.x) dst[i] = src[i];
+        __syncthreads();
+    }
+    if (wave >= N) return;
+    float acc[M][2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const f32x2 a = dec2<F>(d[i], false), b = dec2<F>(d[i], true);
-                w[4 * i] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = b.x; w[4 * i + 3] = b.y;
-            }
+    for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
+    while (true) {
+        u32x4 q[CPL];
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) q[u] = qn[u];
+        // The pair after (r, gi), loaded now.
+        uint32_t rn = r, gn = gi + 1;
+        if (gn == gpr) {
+            gn = 0;
+            rn = r + waves;
+        }
+        if (rn < N) load(rn, gn, qn);
+
+        const uint32_t c0 = gi * 64 * CPL + lane;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const uint32_t ch = c0 + u * 64;
+            if (ragged && ch >= nch) continue;
+            uint32_t w[8];
+            decode16<F>(q[u], w);
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + (size_t)m * K) + 2 * c;
-                const u32x4 x0 = xr[0], x1 = xr[1];
-                const uint32_t xd[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                float a = acc[m];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    a = __builtin_fmaf(bf_lo(xd[i]), w[2 * i], a);
-                    a = __builtin_fmaf(bf_hi(xd[i]), w[2 * i + 1], a);
+                u32x4 xa, xb;
+                if constexpr (XLDS) {
+                    const u32x4 *xp = reinterpret_cast<const u32x4 *>(xs) + (m * nch + ch) * 2;
+                    xa = xp[0];
+                    xb = xp[1];
+                } else {
+                    const u32x4 *xp = reinterpret_cast<const u32x4 *>(x + (size_t)m * K) + ch * 2;
+                    xa = xp[0];
+                    xb = xp[1];
                 }
-                acc[m] = a;
+                acc[m][0] = dot2(w[0], xa.x, acc[m][0]);
+                acc[m][1] = dot2(w[1], xa.y, acc[m][1]);
+                acc[m][0] = dot2(w[2], xa.z, acc[m][0]);
+                acc[m][1] = dot2(w[3], xa.w, acc[m][1]);
+                acc[m][0] = dot2(w[4], xb.x, acc[m][0]);
+                acc[m][1] = dot2(w[5], xb.y, acc[m][1]);
+                acc[m][0] = dot2(w[6], xb.z, acc[m][0]);
+                acc[m][1] = dot2(w[7], xb.w, acc[m][1]);
             }
         }
-        const float s = scales ? scales[n] : 1.0f;
+        if (gi + 1 == gpr) {   // end of row r: reduce across the wave and store
+            const float s = scales ? scales[r] : 1.0f;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float t = wave_sum_f32(acc[m]);
-            if (lane == 0) y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(t * s);
+            for (int m = 0; m < M; ++m) {
+                const float t = wave_sum_f32(acc[m][0] + acc[m][1]);
+                if (lane == m) y[(size_t)m * N + r] = (uint16_t)f32_to_bf16_bits(t * s);
+                acc[m][0] = acc[m][1] = 0.0f;
+            }
         }
+        if (rn >= N) break;
+        r = rn;
+        gi = gn;
     }
 }
 
@@ -280,16 +350,33 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
         return RENG_HIP_OK;
     }
     if (M <= 4) {
-        const uint32_t waves_per_block = 4;
-        uint32_t blocks = (N + waves_per_block - 1) / waves_per_block;
+        // Rows divide evenly over the waves: at most 16 waves per CU, each
+        // taking rows_per_wave rows.
         const uint32_t cap = (uint32_t)device_props().cus * 16;
-        if (blocks > cap) blocks = cap;
+        const uint32_t rpw = (N + cap - 1) / cap;
+        const uint32_t waves = (N + rpw - 1) / rpw;
+        const size_t xbytes = (size_t)M * K * 2;
+        const bool xlds = xbytes <= 64 * 1024;
+        const int threads = 512;
+        const uint32_t blocks = (waves + threads / 64 - 1) / (threads / 64);
+        const size_t lds = xlds ? xbytes : 0;
+        // 7 chunks per lane when a row splits into whole groups of 7 (K a multiple
+        // of 7168, e.g. 14336), else 4.
+        const bool cpl7 = (K / 16) % (64 * 7) == 0;
+#define RENG_GEMV(MM, C, XL)                                                                  \
+    hipLaunchKernelGGL((gemv_w8a16<F, MM, C, XL>), dim3(blocks), dim3(threads), lds, st, x, codes, \
+                       scales, N, K, y)
+#define RENG_GEMV_M(MM)                                                   \
+    if (cpl7) { if (xlds) RENG_GEMV(MM, 7, true); else RENG_GEMV(MM, 7, false); } \
+    else { if (xlds) RENG_GEMV(MM, 4, true); else RENG_GEMV(MM, 4, false); }
         switch (M) {
-            case 1: hipLaunchKernelGGL((gemv_w8a16<F, 1>), dim3(blocks), dim3(256), 0, st, x, codes, scales, N, K, y); break;
-            case 2: hipLaunchKernelGGL((gemv_w8a16<F, 2>), dim3(blocks), dim3(256), 0, st, x, codes, scales, N, K, y); break;
-            case 3: hipLaunchKernelGGL((gemv_w8a16<F, 3>), dim3(blocks), dim3(256), 0, st, x, codes, scales, N, K, y); break;
-            default: hipLaunchKernelGGL((gemv_w8a16<F, 4>), dim3(blocks), dim3(256), 0, st, x, codes, scales, N, K, y); break;
+            case 1: RENG_GEMV_M(1); break;
+            case 2: RENG_GEMV_M(2); break;
+            case 3: RENG_GEMV_M(3); break;
+            default: RENG_GEMV_M(4); break;
         }
+#undef RENG_GEMV_M
+#undef RENG_GEMV
         return check_launch("gemv_w8a16");
     }
     // Larger M: tiles of 64 activation rows.

@@ -6,20 +6,23 @@
 // workgroup owns a row at a time, holds it in registers between the two
 // phases and so reads HBM once: rows*cols*(in_bytes + 1) + 4*rows bytes.
 //
-// Fast path (a row whose scale s and 1/s are normal f32 and that holds no NaN):
-//   r = RN(1/s); if r*s == 1 exactly, x*r IS RN(x/s) and one conversion suffices.
-//   Otherwise r_lo = r - 1ulp <= 1/s <= r_hi = r + 1ulp, so by monotonicity of
-//   rounding RN(x*r_lo) <= RN(x/s) <= RN(x*r_hi) in magnitude; the fp8 code is
-//   monotone in magnitude, so when both ends give the same code it is the code
-//   of RN(x/s). The two ends go through v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32
-//   (OCP e4m3 / e5m2, round to nearest even), which agree with reng-fp8's
-//   encoder on every input of magnitude <= max finite (240 / 57344): checked
-//   on all 2^32 patterns by reng_hip_verify_hw_convert. Inputs that could
-//   exceed that range are clamped first with v_med3 (saturation is monotone).
-//   A lane whose ends disagree (an fp8 midpoint within ~2 ulps; a few in a
-//   million) recomputes its vector with the IEEE divide and the exact encoder.
-// Slow rows (NaN present, s = inf / 0 / subnormal) use the IEEE divide and the
-// exact encoder for every element, with x86's NaN semantics.
+// Fast path (a row with no NaN and a finite non-zero scale s, subnormal s
+// included): q = RN32(x * RN64(1/s)) computed in f64 IS the IEEE f32 quotient
+// RN32(x / s) that the reference encodes, for every finite x:
+//   * x * RN64(1/s) is within |z| * 2^-52 of z = x / s (two f64 roundings);
+//   * the quotient of two 24-bit floats is never an f32 midpoint, and when it
+//     is not one it lies more than ulp(z) * 2^-25 >= |z| * 2^-49 away from
+//     every midpoint (z - t = (X * 2^a - T * S * 2^b) / (S * 2^c) with integer
+//     significands X, S < 2^24 and a 25-bit midpoint significand T), so the f64
+//     value rounds to the same f32 as z does.
+// The f32 quotient then goes through v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 (OCP
+// e4m3 / e5m2, round to nearest even), which agree with reng-fp8's encoder on
+// every input of magnitude below the first out-of-range midpoint (248 /
+// 61440): checked on all 2^32 patterns by reng_hip_verify_hw_convert. Inputs
+// that could reach that range (HW and UNIT scales, or a backoff above 1) are
+// clamped first with v_med3 (saturation is monotone).
+// Slow rows (a NaN present, s = inf or 0) use the IEEE divide and the exact
+// integer encoder for every element, with x86's NaN semantics.
 #include "common.h"
 #include "quantize.h"
 
@@ -53,6 +56,13 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t *red) {
     }
 }
 
+// RN32(x * R) through f64: R = RN64(1/s), the product and the narrowing are
+// each rounded to nearest even.
+__device__ __forceinline__ float quot(float x, double R) { return (float)((double)x * R); }
+
+__device__ __forceinline__ float bf_lo(uint32_t d) { return __uint_as_float(d << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t d) { return __uint_as_float(d & 0xffff0000u); }
+
 template <typename InT>
 struct InTraits;
 template <>
@@ -80,32 +90,50 @@ __device__ __forceinline__ float row_scale(uint32_t mbits, int scheme, float ful
     return fixed_scale ? fixed_scale[mi] : 1.0f;
 }
 
-// One workgroup (WAVES waves) per row at a time, VPT 16-byte vectors per thread
-// held in registers. Requires: 16-byte aligned rows, cols a multiple of EPV,
-// codes rows aligned to the store width.
-template <typename InT, int F, int VPT, int WAVES, bool CLAMP>
+// One row per workgroup (WAVES waves) at a time, VPT 16-byte vectors per thread
+// held in registers between the absmax and the encode. Requires 16-byte
+// aligned rows, cols a multiple of EPV and codes rows aligned to the store
+// width. FULL: every row fills exactly VPT * 64 * WAVES vectors (no tail
+// predication).
+template <typename InT, int F, int VPT, int WAVES, bool CLAMP, bool FULL>
 __global__ __launch_bounds__(64 * WAVES) void quantize_rows_fast(QBatch B, int scheme, float full,
                                                                   const float *__restrict__ fixed_scale,
                                                                   const uint32_t *__restrict__ fixed_bias) {
     using IT = InTraits<InT>;
     constexpr int EPV = IT::EPV;
+    constexpr int CPV = EPV / 4;                 // code dwords per vector: 2 (bf16), 1 (f32)
     constexpr int T = 64 * WAVES;
     __shared__ uint32_t red[WAVES];
     const int tid = threadIdx.x;
-    for (uint64_t g = blockIdx.x; g < B.total_rows; g += gridDim.x) {
-        int mi = 0;
-        while (mi + 1 < B.n && g >= B.m[mi + 1].row_begin) ++mi;
-        const QMat &M = B.m[mi];
-        const uint64_t row = g - M.row_begin;
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const InT *>(M.w) + row * M.ld);
-        const int nvec = (int)(M.cols / EPV);
+    const uint64_t G = gridDim.x;
+    uint64_t g = blockIdx.x;
+    if (g >= B.total_rows) return;
 
-        u32x4 v[VPT];
+    // Row g lives in matrix mi; rows only grow, so the lookup only moves forward.
+    auto locate = [&](uint64_t gg, int &mi) {
+        while (mi + 1 < B.n && gg >= B.m[mi + 1].row_begin) ++mi;
+    };
+    auto row_src = [&](uint64_t gg, int mi) {
+        const QMat &M = B.m[mi];
+        return reinterpret_cast<const u32x4 *>(static_cast<const InT *>(M.w) + (gg - M.row_begin) * M.ld);
+    };
+    auto load = [&](const u32x4 *src, int nvec, u32x4 (&v)[VPT]) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int i = j * T + tid;
-            v[j] = i < nvec ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+            if (FULL || i < nvec) v[j] = __builtin_nontemporal_load(src + i);
+            else v[j] = u32x4{0u, 0u, 0u, 0u};
         }
+    };
+
+    int mi = 0;
+    locate(g, mi);
+    u32x4 v[VPT];
+    load(row_src(g, mi), (int)(B.m[mi].cols / EPV), v);
+    for (; g < B.total_rows; g += G) {
+        const QMat &M = B.m[mi];
+        const uint64_t row = g - M.row_begin;
+        const int nvec = (int)(M.cols / EPV);
 
         // Phase 1: row absmax on the magnitude bits (NaN patterns sort above inf).
         uint32_t mx = 0;
@@ -122,12 +150,9 @@ __global__ __launch_bounds__(64 * WAVES) void quantize_rows_fast(QBatch B, int s
         } else {
 #pragma unroll
             for (int j = 0; j < VPT; ++j) {
-                const uint32_t d[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t a = d[k] & 0x7fffffffu;
-                    mx = mx > a ? mx : a;
-                }
+                const uint32_t a0 = v[j].x & 0x7fffffffu, a1 = v[j].y & 0x7fffffffu;
+                const uint32_t a2 = v[j].z & 0x7fffffffu, a3 = v[j].w & 0x7fffffffu;
+                mx = max(max(mx, max(a0, a1)), max(a2, a3));
             }
         }
         mx = block_max<WAVES>(mx, red);
@@ -158,65 +183,57 @@ __global__ __launch_bounds__(64 * WAVES) void quantize_rows_fast(QBatch B, int s
                 *M.exp_bias = fixed_bias ? fixed_bias[mi] : (uint32_t)Fp8<F>::BIAS;
         }
 
-        // Phase 2: encode from registers.
-        uint8_t *dst = M.codes + row * M.cols;
-        const bool fast = !has_nan && s >= 0x1p-125f && s <= 0x1p125f;
+        // Phase 2: codes from registers. q = RN32(x * RN64(1/s)) equals the
+        // IEEE f32 quotient RN32(x / s) for every finite x and every finite
+        // non-zero s (see the top of this file), so each code is one f64
+        // multiply and one hardware conversion.
+        uint32_t c[VPT][CPV];
+        const bool fast = !has_nan && s > 0.0f && s < __builtin_inff();
         if (fast) {
-            const float r = 1.0f / s;
-            const bool exact = __builtin_fmaf(r, s, -1.0f) == 0.0f;
-            const float r_hi = exact ? r : __uint_as_float(__float_as_uint(r) + 1u);
-            const float r_lo = exact ? r : __uint_as_float(__float_as_uint(r) - 1u);
+            const double R = 1.0 / (double)s;
 #pragma unroll
             for (int j = 0; j < VPT; ++j) {
-                const int i = j * T + tid;
-                if (i >= nvec) continue;
                 const uint32_t d[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
                 if constexpr (sizeof(InT) == 2) {
-                    float x[8];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        x[2 * k] = __uint_as_float(d[k] << 16);
-                        x[2 * k + 1] = __uint_as_float(d[k] & 0xffff0000u);
-                    }
-                    uint32_t h0 = cvt4<F, CLAMP>(x[0] * r_hi, x[1] * r_hi, x[2] * r_hi, x[3] * r_hi);
-                    uint32_t h1 = cvt4<F, CLAMP>(x[4] * r_hi, x[5] * r_hi, x[6] * r_hi, x[7] * r_hi);
-                    if (!exact) {
-                        const uint32_t l0 = cvt4<F, CLAMP>(x[0] * r_lo, x[1] * r_lo, x[2] * r_lo, x[3] * r_lo);
-                        const uint32_t l1 = cvt4<F, CLAMP>(x[4] * r_lo, x[5] * r_lo, x[6] * r_lo, x[7] * r_lo);
-                        if ((h0 ^ l0) | (h1 ^ l1)) {
-                            h0 = exact4<F>(x[0], x[1], x[2], x[3], s);
-                            h1 = exact4<F>(x[4], x[5], x[6], x[7], s);
-                        }
-                    }
-                    __builtin_nontemporal_store(u32x2{h0, h1}, reinterpret_cast<u32x2 *>(dst) + i);
+                    c[j][0] = cvt4<F, CLAMP>(quot(bf_lo(d[0]), R), quot(bf_hi(d[0]), R),
+                                             quot(bf_lo(d[1]), R), quot(bf_hi(d[1]), R));
+                    c[j][1] = cvt4<F, CLAMP>(quot(bf_lo(d[2]), R), quot(bf_hi(d[2]), R),
+                                             quot(bf_lo(d[3]), R), quot(bf_hi(d[3]), R));
                 } else {
-                    const float x0 = __uint_as_float(d[0]), x1 = __uint_as_float(d[1]);
-                    const float x2 = __uint_as_float(d[2]), x3 = __uint_as_float(d[3]);
-                    uint32_t h = cvt4<F, CLAMP>(x0 * r_hi, x1 * r_hi, x2 * r_hi, x3 * r_hi);
-                    if (!exact) {
-                        const uint32_t l = cvt4<F, CLAMP>(x0 * r_lo, x1 * r_lo, x2 * r_lo, x3 * r_lo);
-                        if (h ^ l) h = exact4<F>(x0, x1, x2, x3, s);
-                    }
-                    __builtin_nontemporal_store(h, reinterpret_cast<uint32_t *>(dst) + i);
+                    c[j][0] = cvt4<F, CLAMP>(quot(__uint_as_float(d[0]), R), quot(__uint_as_float(d[1]), R),
+                                             quot(__uint_as_float(d[2]), R), quot(__uint_as_float(d[3]), R));
                 }
             }
         } else {
+            // Slow row: a NaN is present, or s is infinite or zero; the IEEE
+            // divide with x86's NaN semantics for every element.
 #pragma unroll
             for (int j = 0; j < VPT; ++j) {
-                const int i = j * T + tid;
-                if (i >= nvec) continue;
                 const uint32_t d[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
                 if constexpr (sizeof(InT) == 2) {
-                    const uint32_t h0 = exact4<F>(IT::f(d[0] & 0xffffu), IT::f(d[0] >> 16),
-                                                  IT::f(d[1] & 0xffffu), IT::f(d[1] >> 16), s);
-                    const uint32_t h1 = exact4<F>(IT::f(d[2] & 0xffffu), IT::f(d[2] >> 16),
-                                                  IT::f(d[3] & 0xffffu), IT::f(d[3] >> 16), s);
-                    reinterpret_cast<u32x2 *>(dst)[i] = u32x2{h0, h1};
+                    c[j][0] = exact4<F>(bf_lo(d[0]), bf_hi(d[0]), bf_lo(d[1]), bf_hi(d[1]), s);
+                    c[j][1] = exact4<F>(bf_lo(d[2]), bf_hi(d[2]), bf_lo(d[3]), bf_hi(d[3]), s);
                 } else {
-                    reinterpret_cast<uint32_t *>(dst)[i] =
-                        exact4<F>(IT::f(d[0]), IT::f(d[1]), IT::f(d[2]), IT::f(d[3]), s);
+                    c[j][0] = exact4<F>(__uint_as_float(d[0]), __uint_as_float(d[1]),
+                                        __uint_as_float(d[2]), __uint_as_float(d[3]), s);
                 }
             }
+        }
+        uint8_t *dst = M.codes + row * M.cols;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int i = j * T + tid;
+            if (FULL || i < nvec) {
+                if constexpr (CPV == 2)
+                    __builtin_nontemporal_store(u32x2{c[j][0], c[j][1]}, reinterpret_cast<u32x2 *>(dst) + i);
+                else
+                    __builtin_nontemporal_store(c[j][0], reinterpret_cast<uint32_t *>(dst) + i);
+            }
+        }
+
+        if (g + G < B.total_rows) {
+            locate(g + G, mi);
+            load(row_src(g + G, mi), (int)(B.m[mi].cols / EPV), v);
         }
     }
 }
@@ -335,73 +352,60 @@ namespace {
 
 struct FastCfg {
     int vpt, waves;
+    bool full;
 };
 
-// Vectors per thread and waves per row for a row of nvec 16-byte vectors:
-// the least padding, then the fewest waves (a single wave needs no LDS).
+// Exact fits (no tail predication) for the row widths of the Llama / Qwen
+// shapes: bf16 1024, 2048, 3584, 4096, 5120, 8192, 14336, 16384, 27648 and
+// f32 2048, 8192 columns.
+constexpr FastCfg FULL_CFGS[] = {{8, 1, true}, {7, 1, true}, {7, 4, true}, {5, 2, true}, {8, 2, true},
+                                 {8, 4, true}, {9, 6, true}, {2, 1, true}, {4, 1, true}};
+
 FastCfg pick_cfg(uint64_t nvec) {
-    static const int VPTS[] = {1, 2, 4, 5, 6, 7, 8};
-    FastCfg best{0, 0};
-    uint64_t best_waste = ~0ull;
-    for (int vpt : VPTS) {
-        uint64_t waves = (nvec + 64ull * vpt - 1) / (64ull * vpt);
-        if (waves < 1) waves = 1;
-        if (waves > 16) continue;
-        if (waves == 3 || waves == 5 || waves == 6 || waves == 7 || (waves > 8 && waves != 16)) {
-            // keep the instantiated set small: 1, 2, 4, 8, 16 waves
-            uint64_t w2 = 1;
-            while (w2 < waves) w2 <<= 1;
-            waves = w2;
-        }
-        const uint64_t waste = waves * 64ull * vpt - nvec;
-        if (waste < best_waste || (waste == best_waste && (int)waves < best.waves)) {
-            best_waste = waste;
-            best = FastCfg{vpt, (int)waves};
-        }
+    for (const FastCfg &c : FULL_CFGS)
+        if ((uint64_t)c.vpt * 64 * c.waves == nvec) return c;
+    if (nvec <= 512) {
+        int vpt = 1;
+        while ((uint64_t)vpt * 64 < nvec) vpt <<= 1;
+        return FastCfg{vpt, 1, false};
     }
-    return best;
+    int waves = 1;
+    while ((uint64_t)waves * 512 < nvec) waves <<= 1;
+    if (waves > 16) return FastCfg{0, 0, false};
+    return FastCfg{8, waves, false};
 }
 
-template <typename InT, int F, int VPT, int WAVES, bool CLAMP>
+int encode_key(const FastCfg &c) { return c.vpt * 1000 + c.waves * 10 + (c.full ? 1 : 0); }
+
+// Waves per CU for the register-resident kernel: enough rows in flight to keep
+// HBM busy, few enough that the rows being read and written at one time stay
+// close together (measured on MI355X: 8 waves per CU beat full occupancy).
+constexpr int QUANT_WAVES_PER_CU = 8;
+
+template <typename InT, int F, int VPT, int WAVES, bool CLAMP, bool FULL>
 int launch_fast_t(const QBatch &b, int scheme, float full, const float *fs, const uint32_t *fb,
                   hipStream_t st) {
-    auto kern = quantize_rows_fast<InT, F, VPT, WAVES, CLAMP>;
-    int per_cu = 0;
-    RENG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * WAVES, 0));
-    if (per_cu < 1) per_cu = 1;
-    uint64_t grid = (uint64_t)device_props().cus * per_cu;
+    auto kern = quantize_rows_fast<InT, F, VPT, WAVES, CLAMP, FULL>;
+    uint64_t grid = (uint64_t)device_props().cus * ((QUANT_WAVES_PER_CU + WAVES - 1) / WAVES);
     if (grid > b.total_rows) grid = b.total_rows;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * WAVES), 0, st, b, scheme, full, fs, fb);
     return check_launch("quantize_rows_fast");
 }
 
-template <typename InT, int F, int VPT, bool CLAMP>
-int launch_fast_w(int waves, const QBatch &b, int scheme, float full, const float *fs,
-                  const uint32_t *fb, hipStream_t st) {
-    switch (waves) {
-        case 1: return launch_fast_t<InT, F, VPT, 1, CLAMP>(b, scheme, full, fs, fb, st);
-        case 2: return launch_fast_t<InT, F, VPT, 2, CLAMP>(b, scheme, full, fs, fb, st);
-        case 4: return launch_fast_t<InT, F, VPT, 4, CLAMP>(b, scheme, full, fs, fb, st);
-        case 8: return launch_fast_t<InT, F, VPT, 8, CLAMP>(b, scheme, full, fs, fb, st);
-        case 16: return launch_fast_t<InT, F, VPT, 16, CLAMP>(b, scheme, full, fs, fb, st);
-    }
-    set_error("internal: no kernel for %d waves", waves);
-    return RENG_HIP_EUNSUPPORTED;
-}
-
 template <typename InT, int F, bool CLAMP>
-int launch_fast_v(FastCfg c, const QBatch &b, int scheme, float full, const float *fs,
-                  const uint32_t *fb, hipStream_t st) {
-    switch (c.vpt) {
-        case 1: return launch_fast_w<InT, F, 1, CLAMP>(c.waves, b, scheme, full, fs, fb, st);
-        case 2: return launch_fast_w<InT, F, 2, CLAMP>(c.waves, b, scheme, full, fs, fb, st);
-        case 4: return launch_fast_w<InT, F, 4, CLAMP>(c.waves, b, scheme, full, fs, fb, st);
-        case 5: return launch_fast_w<InT, F, 5, CLAMP>(c.waves, b, scheme, full, fs, fb, st);
-        case 6: return launch_fast_w<InT, F, 6, CLAMP>(c.waves, b, scheme, full, fs, fb, st);
-        case 7: return launch_fast_w<InT, F, 7, CLAMP>(c.waves, b, scheme, full, fs, fb, st);
-        case 8: return launch_fast_w<InT, F, 8, CLAMP>(c.waves, b, scheme, full, fs, fb, st);
+int launch_fast(int key, const QBatch &b, int scheme, float full, const float *fs,
+                const uint32_t *fb, hipStream_t st) {
+#define RENG_Q(V, W, FU)                                                                       \
+    case V * 1000 + W * 10 + FU:                                                                \
+        return launch_fast_t<InT, F, V, W, CLAMP, FU>(b, scheme, full, fs, fb, st);
+    switch (key) {
+        RENG_Q(8, 1, 1) RENG_Q(7, 1, 1) RENG_Q(7, 4, 1) RENG_Q(5, 2, 1) RENG_Q(8, 2, 1)
+        RENG_Q(8, 4, 1) RENG_Q(9, 6, 1) RENG_Q(2, 1, 1) RENG_Q(4, 1, 1)
+        RENG_Q(1, 1, 0) RENG_Q(2, 1, 0) RENG_Q(4, 1, 0) RENG_Q(8, 1, 0) RENG_Q(8, 2, 0)
+        RENG_Q(8, 4, 0) RENG_Q(8, 8, 0) RENG_Q(8, 16, 0)
     }
-    set_error("internal: no kernel for %d vectors per thread", c.vpt);
+#undef RENG_Q
+    set_error("internal: no quantize kernel for configuration %d", key);
     return RENG_HIP_EUNSUPPORTED;
 }
 
@@ -409,9 +413,8 @@ template <typename InT, int F>
 int launch_group(const QBatch &b, int key, int scheme, float full, bool clamp, const float *fs,
                  const uint32_t *fb, hipStream_t st) {
     if (key >= 0) {
-        const FastCfg c{key / 100, key % 100};
-        return clamp ? launch_fast_v<InT, F, true>(c, b, scheme, full, fs, fb, st)
-                     : launch_fast_v<InT, F, false>(c, b, scheme, full, fs, fb, st);
+        return clamp ? launch_fast<InT, F, true>(key, b, scheme, full, fs, fb, st)
+                     : launch_fast<InT, F, false>(key, b, scheme, full, fs, fb, st);
     }
     uint64_t grid = (uint64_t)device_props().cus * 8;
     if (grid > b.total_rows) grid = b.total_rows;
@@ -430,7 +433,7 @@ int launch_absmax(const QBatch &b, float *out, uint32_t *tmax, hipStream_t st) {
 
 }  // namespace
 
-// The register-resident kernel configuration of a matrix (vpt * 100 + waves),
+// The register-resident kernel configuration of a matrix (encode_key),
 // or -1 when it must take the generic kernel (misaligned rows or codes, cols
 // not a multiple of the vector width, rows wider than 16 waves x 8 vectors).
 int fast_key(const QMat &m, int dtype) {
@@ -441,10 +444,8 @@ int fast_key(const QMat &m, int dtype) {
     if ((reinterpret_cast<uintptr_t>(m.w) & 15) != 0) return -1;
     if ((m.ld * eb) % 16 != 0) return -1;
     if ((reinterpret_cast<uintptr_t>(m.codes) & (store - 1)) != 0) return -1;
-    const uint64_t nvec = m.cols / epv;
-    if (nvec > 16ull * 64 * 8) return -1;
-    const FastCfg c = pick_cfg(nvec);
-    return c.vpt > 0 ? c.vpt * 100 + c.waves : -1;
+    const FastCfg c = pick_cfg(m.cols / epv);
+    return c.vpt > 0 ? encode_key(c) : -1;
 }
 
 int launch_quantize_group(const QBatch &b, int dtype, int format, int scheme, float backoff,
