@@ -287,6 +287,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--extended", action="store_true", help="also the full Qwen2.5-32B quantize")
+    ap.add_argument("--part", default="all", choices=["all", "quantize", "gemv", "skinny", "prefill", "f32"],
+                    help="run one part only (for profiling); the JSON line is printed for 'all' and 'quantize'")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="copy 1 GiB device-to-device three times first: a kernel of known traffic that "
+                         "scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -302,6 +307,27 @@ def main():
     torch.cuda.set_device(0)
     R.lib()
     log("device:", R.device_info())
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.int32, device="cuda").random_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    if args.part not in ("all", "quantize"):
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(99)
+        if args.part == "gemv":
+            out = [bench_w8a16(torch, R, gen, 1, 14336, 4096), bench_w8a16(torch, R, gen, 1, 4096, 14336)]
+        elif args.part == "skinny":
+            out = [bench_w8a16(torch, R, gen, M, N, K) for M in (8, 64) for _, N, K in QWEN_7B]
+        elif args.part == "prefill":
+            out = [bench_fp8_gemm(torch, R, gen, 1024, N, K) for N, K in ((5120, 5120), (1024, 5120),
+                                                                           (27648, 5120), (5120, 27648))]
+        else:
+            out = [bench_f32_quantize(torch, R, gen)]
+        log(json.dumps(out))
+        return
     t0 = time.perf_counter()
     ws = WeightSet(torch, LLAMA_8B, 32, seed=1234)
     torch.cuda.synchronize()
@@ -329,7 +355,7 @@ def main():
         log(f"cpu baseline {cpu['value']} GB/s; parity {parity}")
 
     extras = {}
-    if not args.no_extras:
+    if not args.no_extras and args.part == "all":
         other = "e5m2" if args.format == "e4m3" else "e4m3"
         r2 = time_quantize(torch, R, ws, other, max(3, args.steps // 4), 1)
         extras[f"quantize_{other}_GBps"] = round(r2["gbps"], 1)
