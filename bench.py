@@ -190,7 +190,9 @@ def graph_time(torch, fn, n_launch, reps=3):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # Capture on the warm-up stream: per-stream buffers the library keeps (the
+    # split-K workspace) already exist there, so nothing allocates inside the capture.
+    with torch.cuda.graph(g, stream=s):
         for i in range(n_launch):
             fn(i)
     g.replay()

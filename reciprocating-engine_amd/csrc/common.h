@@ -208,6 +208,23 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return v;
 }
 
+// Sum over the 64 lanes with DPP moves (no LDS round trip): row_shr 1, 2, 4, 8
+// leave each 16-lane row's sum in its lane 15; row_bcast 15 and 31 carry the
+// rows into lane 63, which is read back as a scalar for every lane.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_mov<0x111, 0xf>(v);   // row_shr:1
+    v += dpp_mov<0x112, 0xf>(v);   // row_shr:2
+    v += dpp_mov<0x114, 0xf>(v);   // row_shr:4
+    v += dpp_mov<0x118, 0xf>(v);   // row_shr:8
+    v += dpp_mov<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_mov<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -16,6 +16,10 @@
 // The reference semantics are gemm_cpu over Quantized::dequantize
 // (crates/reng-model/src/bin/fp8_probe.rs:55-67) and the per-channel scaleB of
 // fp8_gemm_bf16 (crates/reng-synapse/src/fp8.rs:295-331).
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "common.h"
 #include "gemm.h"
 
@@ -86,7 +90,7 @@ __device__ __forceinline__ void decode16(const u32x4 &q, uint32_t (&w)[8]) {
 // are staged once per block in LDS as bf16 (XLDS) or read through the caches.
 // Codes decode to bf16 pairs in registers and meet the activation in
 // v_dot2_f32_bf16 (f32 accumulation).
-template <int F, int M, int CPL, bool XLDS>
+template <int F, int M, int CPL, bool XLDS, bool RAGGED>
 __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x,
                                                   const uint8_t *__restrict__ codes,
                                                   const float *__restrict__ scales, uint32_t N,
@@ -97,15 +101,18 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
     const uint32_t waves = gridDim.x * (blockDim.x >> 6);
     const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (tid >> 6);
     const uint32_t gpr = (nch + 64 * CPL - 1) / (64 * CPL);   // groups per row
-    const bool ragged = nch % (64 * CPL) != 0;
 
+    // Loads are unconditional (indices clamped into the matrix) so the wait
+    // before each use covers exactly the loads issued before it; a ragged
+    // tail's surplus chunks are zeroed after the load.
     auto load = [&](uint32_t r, uint32_t gi, u32x4 (&q)[CPL]) {
+        r = r < N ? r : N - 1;
         const u32x4 *wr = reinterpret_cast<const u32x4 *>(codes + (size_t)r * K);
         const uint32_t c0 = gi * 64 * CPL + lane;
 #pragma unroll
         for (int u = 0; u < CPL; ++u) {
             const uint32_t ch = c0 + u * 64;
-            q[u] = (!ragged || ch < nch) ? __builtin_nontemporal_load(wr + ch) : u32x4{0u, 0u, 0u, 0u};
+            q[u] = __builtin_nontemporal_load(wr + (RAGGED && ch >= nch ? nch - 1 : ch));
         }
     };
 
@@ -133,15 +140,19 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
             gn = 0;
             rn = r + waves;
         }
-        if (rn < N) load(rn, gn, qn);
+        load(rn, gn, qn);
 
         const uint32_t c0 = gi * 64 * CPL + lane;
 #pragma unroll
         for (int u = 0; u < CPL; ++u) {
-            const uint32_t ch = c0 + u * 64;
-            if (ragged && ch >= nch) continue;
+            uint32_t ch = c0 + u * 64;
             uint32_t w[8];
             decode16<F>(q[u], w);
+            if (RAGGED && ch >= nch) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[i] = 0u;
+                ch = nch - 1;
+            }
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 u32x4 xa, xb;
@@ -168,7 +179,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
             const float s = scales ? scales[r] : 1.0f;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float t = wave_sum_f32(acc[m][0] + acc[m][1]);
+                const float t = wave_sum_dpp(acc[m][0] + acc[m][1]);
                 if (lane == m) y[(size_t)m * N + r] = (uint16_t)f32_to_bf16_bits(t * s);
                 acc[m][0] = acc[m][1] = 0.0f;
             }
@@ -181,71 +192,247 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 
 // ------------------------------------------------------------------ skinny GEMM
 
-// Block = 4 waves on one 16-row tile of W; wave w takes the K chunks
-// c = w, w + 4, ... of 128 codes. Lane l owns row n0 + l % 16 and, within a
-// chunk, codes [32 * (l / 16), +32): four MFMA k-slices of 8. The activation
-// fragment uses the same k assignment, so the k order inside an MFMA is a
-// permutation shared by both operands and the sum is unchanged.
-template <int F, int MT>
+// 4 < M <= 64 on bf16 MFMA (v_mfma_f32_16x16x32_bf16), D[n][m] = W[n][k] X[m][k]:
+// codes are the A operand (16 output rows x 32 k per MFMA, decoded to bf16 in
+// registers), the activation the B operand (16 columns m).
+//
+// Block = 4 waves on BN = 64 * AF rows; wave w owns AF fragments of 16 rows.
+// K is walked in steps of 128 codes. Each step's activation tile x[0:16MT,
+// k0:k0+128] is staged once per block in LDS (double-buffered, one barrier per
+// step) and read by every wave, so the activation crosses L2 once per 64*AF
+// rows. Within a step, lane l owns row (l % 16) of each fragment and the 32
+// consecutive codes [32 (l / 16), +32): four MFMA k-slices of 8. The B fragment
+// uses the same k assignment (a permutation of k shared by both operands).
+// The next step's codes and activation tile are loaded before the current
+// step's MFMAs. Split-K over blockIdx.y writes f32 partials to part[y][m][n]
+// (summed in a fixed order by skinny_epilogue); with one split the block
+// writes bf16 y directly.
+constexpr int SK_STEP = 128, SK_PAD = 8;
+
+template <int F, int MT, int AF>
 __global__ __launch_bounds__(256) void skinny_w8a16(const uint16_t *__restrict__ x,
                                                     const uint8_t *__restrict__ codes,
                                                     const float *__restrict__ scales, uint32_t M,
-                                                    uint32_t N, uint32_t K, uint16_t *__restrict__ y) {
-    __shared__ float red[4][MT][64][4];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const uint32_t n0 = blockIdx.x * 16;
-    const int r = lane & 15, g = lane >> 4;
-    const uint32_t nrow = n0 + r < N ? n0 + r : N - 1;   // clamp reads; stores are masked
-    const uint8_t *wr = codes + (size_t)nrow * K;
-    f32x4 acc[MT];
+                                                    uint32_t N, uint32_t K, uint32_t steps_per_split,
+                                                    uint16_t *__restrict__ y, float *__restrict__ part) {
+    constexpr int XR = 16 * MT;                 // activation rows in the tile
+    constexpr int XS = SK_STEP + SK_PAD;        // LDS row stride, bf16
+    constexpr int XV = XR * SK_STEP / 8 / 256;  // 16-byte activation vectors per thread per step
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][XR * XS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const uint32_t n0 = blockIdx.x * (64 * AF) + wave * (16 * AF);
+    const uint32_t steps = K / SK_STEP;
+    const uint32_t s0 = blockIdx.y * steps_per_split;
+    const uint32_t s1 = s0 + steps_per_split < steps ? s0 + steps_per_split : steps;
+
+    // This thread's activation vectors of a step: vector v = it * 256 + tid of
+    // the XR x 16 vectors, row v / 16, 8 bf16 at column (v % 16) * 8.
+    auto load_x = [&](uint32_t st, u32x4 (&xv)[XV]) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t nchunks = K / 128;
-    for (uint32_t c = wave; c < nchunks; c += 4) {
-        const uint32_t k0 = c * 128 + 32 * g;
-        const u32x4 *wp = reinterpret_cast<const u32x4 *>(wr + k0);
-        const u32x4 q0 = __builtin_nontemporal_load(wp), q1 = __builtin_nontemporal_load(wp + 1);
-        const uint32_t d[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        bf16x8 a[4];
+        for (int it = 0; it < XV; ++it) {
+            const int v = it * 256 + tid, row = v >> 4, col = (v & 15) * 8;
+            xv[it] = (uint32_t)row < M ? *reinterpret_cast<const u32x4 *>(x + (size_t)row * K + st * SK_STEP + col)
+                                       : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store_x = [&](int buf, const u32x4 (&xv)[XV]) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const bf16x2 p0 = dec2_bf16<F>(d[2 * s], false), p1 = dec2_bf16<F>(d[2 * s], true);
-            const bf16x2 p2 = dec2_bf16<F>(d[2 * s + 1], false), p3 = dec2_bf16<F>(d[2 * s + 1], true);
-            a[s] = bf16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+        for (int it = 0; it < XV; ++it) {
+            const int v = it * 256 + tid, row = v >> 4, col = (v & 15) * 8;
+            *reinterpret_cast<u32x4 *>(&xs[buf][row * XS + col]) = xv[it];
+        }
+    };
+    auto load_w = [&](uint32_t st, u32x4 (&q)[AF][2]) {
+#pragma unroll
+        for (int f = 0; f < AF; ++f) {
+            uint32_t n = n0 + f * 16 + r16;
+            n = n < N ? n : N - 1;   // clamped reads; stores are masked
+            const u32x4 *wp = reinterpret_cast<const u32x4 *>(codes + (size_t)n * K + st * SK_STEP + 32 * g4);
+            q[f][0] = __builtin_nontemporal_load(wp);
+            q[f][1] = __builtin_nontemporal_load(wp + 1);
+        }
+    };
+
+    f32x4 acc[AF][MT];
+#pragma unroll
+    for (int f = 0; f < AF; ++f)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 q[AF][2], qn[AF][2], xv[XV];
+    load_w(s0, q);
+    load_x(s0, xv);
+    store_x(0, xv);
+    __syncthreads();
+    for (uint32_t st = s0; st < s1; ++st) {
+        const int buf = (st - s0) & 1;
+        const uint32_t nx = st + 1 < s1 ? st + 1 : s1 - 1;   // clamped: no branch around the loads
+        load_w(nx, qn);
+        load_x(nx, xv);
+        bf16x8 a[AF][4];
+#pragma unroll
+        for (int f = 0; f < AF; ++f) {
+            const uint32_t d[8] = {q[f][0].x, q[f][0].y, q[f][0].z, q[f][0].w,
+                                   q[f][1].x, q[f][1].y, q[f][1].z, q[f][1].w};
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                const bf16x2 p0 = dec2_bf16<F>(d[2 * sl], false), p1 = dec2_bf16<F>(d[2 * sl], true);
+                const bf16x2 p2 = dec2_bf16<F>(d[2 * sl + 1], false), p3 = dec2_bf16<F>(d[2 * sl + 1], true);
+                a[f][sl] = bf16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+            }
         }
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            const uint32_t m = t * 16 + r;
-            const uint32_t mm = m < M ? m : M - 1;
-            const u32x4 *xp = reinterpret_cast<const u32x4 *>(x + (size_t)mm * K + k0);
-            u32x4 xv[4] = {xp[0], xp[1], xp[2], xp[3]};
-            if (m >= M) {
+            const uint16_t *xr = &xs[buf][(t * 16 + r16) * XS + 32 * g4];
 #pragma unroll
-                for (int s = 0; s < 4; ++s) xv[s] = u32x4{0u, 0u, 0u, 0u};
+            for (int sl = 0; sl < 4; ++sl) {
+                const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(xr + 8 * sl));
+#pragma unroll
+                for (int f = 0; f < AF; ++f)
+                    acc[f][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[f][sl], b, acc[f][t], 0, 0, 0);
             }
+        }
+        store_x(buf ^ 1, xv);   // buf ^ 1 was last read before the previous barrier
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s], __builtin_bit_cast(bf16x8, xv[s]),
-                                                                 acc[t], 0, 0, 0);
+        for (int f = 0; f < AF; ++f) {
+            q[f][0] = qn[f][0];
+            q[f][1] = qn[f][1];
+        }
+        __syncthreads();
+    }
+    // D of a 16x16 tile: lane l holds column m = l % 16, rows n = 4 * (l / 16) + e.
+#pragma unroll
+    for (int f = 0; f < AF; ++f) {
+        const uint32_t nb = n0 + f * 16 + 4 * g4;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const uint32_t m = t * 16 + r16;
+            if (m >= M) continue;
+            if (part) {
+                float *pp = part + ((size_t)blockIdx.y * M + m) * N;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (nb + e < N) pp[nb + e] = acc[f][t][e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t n = nb + e;
+                    if (n < N) {
+                        const float sc = scales ? scales[n] : 1.0f;
+                        y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[f][t][e] * sc);
+                    }
+                }
+            }
         }
     }
-    // D[i][j] of a 16x16 tile: lane l holds column j = l % 16 (m), rows i = 4 * (l / 16) + e (n).
+}
+
+// M <= 16: independent waves, no LDS and no barrier. A wave owns AF fragments
+// (16 * AF output rows); per 128-code step it reads its codes (prefetched two
+// steps ahead) and the step's 16-column activation fragment (64 bytes per
+// lane, from L2, one step ahead), and issues AF * 4 MFMAs. Split-K over
+// blockIdx.y as in skinny_w8a16.
+template <int F, int AF>
+__global__ __launch_bounds__(256) void skinny_small(const uint16_t *__restrict__ x,
+                                                    const uint8_t *__restrict__ codes,
+                                                    const float *__restrict__ scales, uint32_t M,
+                                                    uint32_t N, uint32_t K, uint32_t steps_per_split,
+                                                    uint16_t *__restrict__ y, float *__restrict__ part) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const uint32_t n0 = (blockIdx.x * 4 + wave) * (16 * AF);
+    if (n0 >= N) return;
+    const uint32_t steps = K / SK_STEP;
+    const uint32_t s0 = blockIdx.y * steps_per_split;
+    const uint32_t s1 = s0 + steps_per_split < steps ? s0 + steps_per_split : steps;
+    const bool mrow = (uint32_t)r16 < M;
+    const uint16_t *xrow = x + (size_t)(mrow ? r16 : 0) * K + 32 * g4;
+
+    auto load_w = [&](uint32_t st, u32x4 (&q)[AF][2]) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[wave][t][lane][e] = acc[t][e];
-    __syncthreads();
-    // 256 threads finish 16 x (16 * MT) outputs.
-    for (int o = threadIdx.x; o < 16 * 16 * MT; o += 256) {
-        const int t = o / 256, rem = o % 256, ln = rem / 4, e = rem % 4;
-        const float v = red[0][t][ln][e] + red[1][t][ln][e] + red[2][t][ln][e] + red[3][t][ln][e];
-        const uint32_t m = t * 16 + (ln & 15);
-        const uint32_t n = n0 + 4 * (ln >> 4) + e;
-        if (m < M && n < N) {
-            const float s = scales ? scales[n] : 1.0f;
-            y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v * s);
+        for (int f = 0; f < AF; ++f) {
+            uint32_t n = n0 + f * 16 + r16;
+            n = n < N ? n : N - 1;
+            const u32x4 *wp = reinterpret_cast<const u32x4 *>(codes + (size_t)n * K + st * SK_STEP + 32 * g4);
+            q[f][0] = __builtin_nontemporal_load(wp);
+            q[f][1] = __builtin_nontemporal_load(wp + 1);
         }
+    };
+    auto load_b = [&](uint32_t st, u32x4 (&b)[4]) {
+        const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow + st * SK_STEP);
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) b[sl] = mrow ? xp[sl] : u32x4{0u, 0u, 0u, 0u};
+    };
+
+    f32x4 acc[AF];
+#pragma unroll
+    for (int f = 0; f < AF; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 q0[AF][2], q1[AF][2], q2[AF][2], b0[4], b1[4];
+    load_w(s0, q0);
+    load_b(s0, b0);
+    load_w(s0 + 1 < s1 ? s0 + 1 : s1 - 1, q1);
+    for (uint32_t st = s0; st < s1; ++st) {
+        // Unconditional prefetches (clamped to the split's last step): no branch,
+        // so each use waits only for the loads issued before it.
+        load_w(st + 2 < s1 ? st + 2 : s1 - 1, q2);
+        load_b(st + 1 < s1 ? st + 1 : s1 - 1, b1);
+#pragma unroll
+        for (int f = 0; f < AF; ++f) {
+            const uint32_t d[8] = {q0[f][0].x, q0[f][0].y, q0[f][0].z, q0[f][0].w,
+                                   q0[f][1].x, q0[f][1].y, q0[f][1].z, q0[f][1].w};
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                const bf16x2 p0 = dec2_bf16<F>(d[2 * sl], false), p1 = dec2_bf16<F>(d[2 * sl], true);
+                const bf16x2 p2 = dec2_bf16<F>(d[2 * sl + 1], false), p3 = dec2_bf16<F>(d[2 * sl + 1], true);
+                const bf16x8 a = bf16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+                acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, b0[sl]), acc[f], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < AF; ++f) {
+            q0[f][0] = q1[f][0];
+            q0[f][1] = q1[f][1];
+            q1[f][0] = q2[f][0];
+            q1[f][1] = q2[f][1];
+        }
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) b0[sl] = b1[sl];
+    }
+#pragma unroll
+    for (int f = 0; f < AF; ++f) {
+        const uint32_t nb = n0 + f * 16 + 4 * g4;
+        if (!mrow) continue;
+        const uint32_t m = r16;
+        if (part) {
+            float *pp = part + ((size_t)blockIdx.y * M + m) * N;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (nb + e < N) pp[nb + e] = acc[f][e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t n = nb + e;
+                if (n < N) {
+                    const float sc = scales ? scales[n] : 1.0f;
+                    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[f][e] * sc);
+                }
+            }
+        }
+    }
+}
+
+// y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the split-K partials summed in order.
+__global__ void skinny_epilogue(const float *__restrict__ part, uint32_t splits, uint32_t M, uint32_t N,
+                                const float *__restrict__ scales, uint16_t *__restrict__ y) {
+    const uint64_t total = (uint64_t)M * N;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < splits; ++k) acc += part[k * total + i];
+        const uint32_t n = (uint32_t)(i % N);
+        const float sc = scales ? scales[n] : 1.0f;
+        y[i] = (uint16_t)f32_to_bf16_bits(acc * sc);
     }
 }
 
@@ -335,6 +522,115 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const uint8_t *__restrict
 
 // ------------------------------------------------------------------ launchers
 
+// Split-K partials live in a grow-only f32 buffer per (device, stream): calls on
+// one stream are ordered, so they can share it; calls on different streams get
+// different buffers. No allocation once a stream has seen its largest product.
+float *split_workspace(size_t floats, hipStream_t st, int *rc) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, std::pair<float *, size_t>> bufs;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(mu);
+    auto &e = bufs[{dev, st}];
+    if (e.second < floats) {
+        if (e.first) {
+            // The old buffer may still be read by work queued on this stream.
+            const hipError_t se = hipStreamSynchronize(st);
+            if (se != hipSuccess) {
+                set_error("hipStreamSynchronize: %s", hipGetErrorString(se));
+                *rc = RENG_HIP_EDEVICE;
+                return nullptr;
+            }
+            (void)hipFree(e.first);
+            e.first = nullptr;
+            e.second = 0;
+        }
+        void *p = nullptr;
+        const hipError_t ae = hipMalloc(&p, floats * sizeof(float));
+        if (ae != hipSuccess) {
+            set_error("hipMalloc(split workspace, %zu bytes): %s", floats * sizeof(float), hipGetErrorString(ae));
+            *rc = RENG_HIP_ENOMEM;
+            return nullptr;
+        }
+        e.first = static_cast<float *>(p);
+        e.second = floats;
+    }
+    *rc = RENG_HIP_OK;
+    return e.first;
+}
+
+struct SplitPlan {
+    uint32_t splits, steps_per_split;
+};
+
+// Split K until the grid has about `want` independent units (blocks or waves).
+SplitPlan plan_splits(uint32_t tiles, uint32_t steps, uint32_t want) {
+    uint32_t splits = (want + tiles - 1) / tiles;
+    const uint32_t max_splits = steps / 2 > 0 ? steps / 2 : 1;
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    const uint32_t sps = (steps + splits - 1) / splits;
+    return SplitPlan{(steps + sps - 1) / sps, sps};
+}
+
+int launch_epilogue(const float *part, uint32_t splits, uint32_t M, uint32_t N, const float *scales,
+                    uint16_t *y, hipStream_t st) {
+    uint64_t blocks = ((uint64_t)M * N + 255) / 256;
+    const uint64_t cap = (uint64_t)device_props().cus * 8;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL(skinny_epilogue, dim3((unsigned)blocks), dim3(256), 0, st, part, splits, M, N, scales, y);
+    return check_launch("skinny_epilogue");
+}
+
+// One launch of the LDS-shared kernel (16 < M <= 64): 128-row blocks (64 for
+// narrow N), split-K until there are ~2 blocks per CU.
+template <int F, int MT, int AF>
+int launch_skinny_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
+                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
+    const uint32_t tiles = (N + 64 * AF - 1) / (64 * AF);
+    const SplitPlan p = plan_splits(tiles, K / SK_STEP, 2u * (uint32_t)device_props().cus);
+    int rc = RENG_HIP_OK;
+    float *part = p.splits > 1 ? split_workspace((size_t)p.splits * M * N, st, &rc) : nullptr;
+    if (rc) return rc;
+    hipLaunchKernelGGL((skinny_w8a16<F, MT, AF>), dim3(tiles, p.splits), dim3(256), 0, st, x, codes, scales, M,
+                       N, K, p.steps_per_split, y, part);
+    rc = check_launch("skinny_w8a16");
+    if (rc == RENG_HIP_OK && part) rc = launch_epilogue(part, p.splits, M, N, scales, y, st);
+    return rc;
+}
+
+// M <= 16: independent waves of 64 rows, split-K until there are ~3 waves per CU.
+template <int F>
+int launch_skinny_small(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
+                        uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
+    constexpr int AF = 4;
+    const uint32_t wave_tiles = (N + 16 * AF - 1) / (16 * AF);
+    const SplitPlan p = plan_splits(wave_tiles, K / SK_STEP, 3u * (uint32_t)device_props().cus);
+    int rc = RENG_HIP_OK;
+    float *part = p.splits > 1 ? split_workspace((size_t)p.splits * M * N, st, &rc) : nullptr;
+    if (rc) return rc;
+    hipLaunchKernelGGL((skinny_small<F, AF>), dim3((wave_tiles + 3) / 4, p.splits), dim3(256), 0, st, x, codes,
+                       scales, M, N, K, p.steps_per_split, y, part);
+    rc = check_launch("skinny_small");
+    if (rc == RENG_HIP_OK && part) rc = launch_epilogue(part, p.splits, M, N, scales, y, st);
+    return rc;
+}
+
+template <int F>
+int launch_skinny(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
+                  uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
+    if (M <= 16) return launch_skinny_small<F>(x, codes, scales, M, N, K, y, st);
+    const bool wide = N >= 1024;
+    switch ((M + 15) / 16) {
+        case 2: return wide ? launch_skinny_t<F, 2, 2>(x, codes, scales, M, N, K, y, st)
+                            : launch_skinny_t<F, 2, 1>(x, codes, scales, M, N, K, y, st);
+        case 3: return wide ? launch_skinny_t<F, 3, 2>(x, codes, scales, M, N, K, y, st)
+                            : launch_skinny_t<F, 3, 1>(x, codes, scales, M, N, K, y, st);
+        default: return wide ? launch_skinny_t<F, 4, 2>(x, codes, scales, M, N, K, y, st)
+                             : launch_skinny_t<F, 4, 1>(x, codes, scales, M, N, K, y, st);
+    }
+}
+
 template <int F>
 int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
@@ -363,12 +659,16 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
         // 7 chunks per lane when a row splits into whole groups of 7 (K a multiple
         // of 7168, e.g. 14336), else 4.
         const bool cpl7 = (K / 16) % (64 * 7) == 0;
-#define RENG_GEMV(MM, C, XL)                                                                  \
-    hipLaunchKernelGGL((gemv_w8a16<F, MM, C, XL>), dim3(blocks), dim3(threads), lds, st, x, codes, \
+        const bool ragged = (K / 16) % (64 * (cpl7 ? 7 : 4)) != 0;
+#define RENG_GEMV(MM, C, XL, RG)                                                                   \
+    hipLaunchKernelGGL((gemv_w8a16<F, MM, C, XL, RG>), dim3(blocks), dim3(threads), lds, st, x, codes, \
                        scales, N, K, y)
-#define RENG_GEMV_M(MM)                                                   \
-    if (cpl7) { if (xlds) RENG_GEMV(MM, 7, true); else RENG_GEMV(MM, 7, false); } \
-    else { if (xlds) RENG_GEMV(MM, 4, true); else RENG_GEMV(MM, 4, false); }
+#define RENG_GEMV_X(MM, C, RG) \
+    if (xlds) RENG_GEMV(MM, C, true, RG); else RENG_GEMV(MM, C, false, RG);
+#define RENG_GEMV_M(MM)                                  \
+    if (cpl7) { RENG_GEMV_X(MM, 7, false) }              \
+    else if (ragged) { RENG_GEMV_X(MM, 4, true) }        \
+    else { RENG_GEMV_X(MM, 4, false) }
         switch (M) {
             case 1: RENG_GEMV_M(1); break;
             case 2: RENG_GEMV_M(2); break;
@@ -376,22 +676,14 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
             default: RENG_GEMV_M(4); break;
         }
 #undef RENG_GEMV_M
+#undef RENG_GEMV_X
 #undef RENG_GEMV
         return check_launch("gemv_w8a16");
     }
-    // Larger M: tiles of 64 activation rows.
+    // Larger M: tiles of up to 64 activation rows on the MFMA kernel.
     for (uint32_t mb = 0; mb < M; mb += 64) {
         const uint32_t mt = M - mb < 64 ? M - mb : 64;
-        const dim3 grid((N + 15) / 16);
-        const uint16_t *xb = x + (size_t)mb * K;
-        uint16_t *yb = y + (size_t)mb * N;
-        switch ((mt + 15) / 16) {
-            case 1: hipLaunchKernelGGL((skinny_w8a16<F, 1>), grid, dim3(256), 0, st, xb, codes, scales, mt, N, K, yb); break;
-            case 2: hipLaunchKernelGGL((skinny_w8a16<F, 2>), grid, dim3(256), 0, st, xb, codes, scales, mt, N, K, yb); break;
-            case 3: hipLaunchKernelGGL((skinny_w8a16<F, 3>), grid, dim3(256), 0, st, xb, codes, scales, mt, N, K, yb); break;
-            default: hipLaunchKernelGGL((skinny_w8a16<F, 4>), grid, dim3(256), 0, st, xb, codes, scales, mt, N, K, yb); break;
-        }
-        const int rc = check_launch("skinny_w8a16");
+        const int rc = launch_skinny<F>(x + (size_t)mb * K, codes, scales, mt, N, K, y + (size_t)mb * N, st);
         if (rc) return rc;
     }
     return RENG_HIP_OK;
