@@ -13,4 +13,9 @@ int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, con
                     int fb, const float *sb, uint32_t nsb, uint32_t M, uint32_t N, uint32_t K,
                     uint16_t *out, hipStream_t st);
 
+// Grow-only f32 scratch for k-split partial sums, one per (device, stream):
+// calls on one stream are ordered and share it. Sets *rc and returns null on
+// failure.
+float *split_workspace(size_t floats, hipStream_t st, int *rc);
+
 }  // namespace reng

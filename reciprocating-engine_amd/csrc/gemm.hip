@@ -8,10 +8,7 @@
 //    (v_cvt_scalef32_pk_bf16_fp8, exact: bf16 holds every e4m3 / e5m2 value),
 //    activations as the B operand; the four waves of a block split K and meet
 //    in LDS.
-// 3. gemm_fp8_scaled: fp8 x fp8 on v_mfma_scale_f32_32x32x64_f8f6f4 (the OCP
-//    fp8 formats, whose finite codes 0x00-0x77 / 0x00-0x7b mean what reng-fp8's
-//    mean), 128x128 block tiles staged through LDS, epilogue
-//    out = acc * sa[m] * sb[n] rounded to bf16.
+// (The fp8 x fp8 product of gemm_fp8_scaled is in gemm_fp8.hip.)
 //
 // The reference semantics are gemm_cpu over Quantized::dequantize
 // (crates/reng-model/src/bin/fp8_probe.rs:55-67) and the per-channel scaleB of
@@ -436,90 +433,6 @@ __global__ void skinny_epilogue(const float *__restrict__ part, uint32_t splits,
     }
 }
 
-// ------------------------------------------------------------------ fp8 x fp8 GEMM
-
-// Block tile 128 (m) x 128 (n), K step 128, 4 waves in a 2 x 2 grid, each wave
-// 64 x 64 = 2 x 2 MFMA tiles of 32 x 32. Operand layout of the 32x32x64 fp8
-// MFMA: lane l holds row (l % 32) and the 32 consecutive k of half l / 32.
-// LDS rows are padded to 144 bytes against bank conflicts.
-constexpr int GB_M = 128, GB_N = 128, GB_K = 128, G_LDS = GB_K + 16;
-
-template <int FA, int FB>
-__global__ __launch_bounds__(256) void gemm_fp8_kernel(const uint8_t *__restrict__ a,
-                                                       const float *__restrict__ sa, uint32_t nsa,
-                                                       const uint8_t *__restrict__ b,
-                                                       const float *__restrict__ sb, uint32_t nsb,
-                                                       uint32_t M, uint32_t N, uint32_t K,
-                                                       uint16_t *__restrict__ out) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds_a[GB_M * G_LDS];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_b[GB_N * G_LDS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const uint32_t m0 = blockIdx.y * GB_M, n0 = blockIdx.x * GB_N;
-    f32x16 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-    for (uint32_t k0 = 0; k0 < K; k0 += GB_K) {
-        // Global -> LDS: 128 rows x 128 bytes per operand = 1024 16-byte vectors; 4 per thread.
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int v = it * 256 + tid;
-            const int row = v >> 3, col = (v & 7) * 16;
-            const uint32_t ga = m0 + row < M ? m0 + row : M - 1;
-            const uint32_t gb = n0 + row < N ? n0 + row : N - 1;
-            const u32x4 va = *reinterpret_cast<const u32x4 *>(a + (size_t)ga * K + k0 + col);
-            const u32x4 vb = *reinterpret_cast<const u32x4 *>(b + (size_t)gb * K + k0 + col);
-            *reinterpret_cast<u32x4 *>(lds_a + row * G_LDS + col) = va;
-            *reinterpret_cast<u32x4 *>(lds_b + row * G_LDS + col) = vb;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int ks = 0; ks < GB_K; ks += 64) {
-            i32x8 fa[2], fb[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint8_t *pa = lds_a + (wm * 64 + i * 32 + (lane & 31)) * G_LDS + ks + 32 * (lane >> 5);
-                const u32x4 a0 = *reinterpret_cast<const u32x4 *>(pa);
-                const u32x4 a1 = *reinterpret_cast<const u32x4 *>(pa + 16);
-                fa[i] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                const uint8_t *pb = lds_b + (wn * 64 + i * 32 + (lane & 31)) * G_LDS + ks + 32 * (lane >> 5);
-                const u32x4 b0 = *reinterpret_cast<const u32x4 *>(pb);
-                const u32x4 b1 = *reinterpret_cast<const u32x4 *>(pb + 16);
-                fb[i] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        fa[i], fb[j], acc[i][j], FA, FB, 0, 0, 0, 0);
-        }
-        __syncthreads();
-    }
-    // D of a 32x32 tile: lane l holds column j = l % 32 (n), rows
-    // i = 8 * (e / 4) + 4 * (l / 32) + e % 4 (m) for e = 0..15.
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t n = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (n >= N) continue;
-            const float sbn = nsb == 0 ? 1.0f : (nsb == 1 ? sb[0] : sb[n]);
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                if (m >= M) continue;
-                const float sam = nsa == 0 ? 1.0f : (nsa == 1 ? sa[0] : sa[m]);
-                out[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][e] * sam * sbn);
-            }
-        }
-}
-
 // ------------------------------------------------------------------ launchers
 
 // Split-K partials live in a grow-only f32 buffer per (device, stream): calls on
@@ -693,21 +606,6 @@ int launch_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales, u
                  uint32_t N, uint32_t K, int format, uint16_t *y, hipStream_t st) {
     return format == RENG_HIP_E4M3 ? launch_w8a16_t<RENG_HIP_E4M3>(x, codes, scales, M, N, K, y, st)
                                    : launch_w8a16_t<RENG_HIP_E5M2>(x, codes, scales, M, N, K, y, st);
-}
-
-int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, const uint8_t *b,
-                    int fb, const float *sb, uint32_t nsb, uint32_t M, uint32_t N, uint32_t K,
-                    uint16_t *out, hipStream_t st) {
-    const dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
-#define RENG_FP8_GEMM(A, B)                                                                     \
-    hipLaunchKernelGGL((gemm_fp8_kernel<A, B>), grid, dim3(256), 0, st, a, sa, nsa, b, sb, nsb, \
-                       M, N, K, out)
-    if (fa == RENG_HIP_E4M3 && fb == RENG_HIP_E4M3) RENG_FP8_GEMM(0, 0);
-    else if (fa == RENG_HIP_E4M3) RENG_FP8_GEMM(0, 1);
-    else if (fb == RENG_HIP_E4M3) RENG_FP8_GEMM(1, 0);
-    else RENG_FP8_GEMM(1, 1);
-#undef RENG_FP8_GEMM
-    return check_launch("gemm_fp8");
 }
 
 }  // namespace reng

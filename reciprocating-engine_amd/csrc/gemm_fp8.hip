@@ -1,0 +1,340 @@
+// gemm_fp8.hip - fp8 x fp8 GEMM on CDNA4 MFMA (gfx950):
+//   out[m, n] = bf16(sum_k dec(a[m, k]) * dec(b[n, k]) * sa[m] * sb[n])
+// with a [M, K] and b [N, K] both K-contiguous (the [K, m] / [K, N] device
+// sizes of gemm_fp8_scaled with transpose_b, crates/reng-synapse/src/fp8.rs:295-331).
+//
+// v_mfma_f32_32x32x64_f8f6f4 on the OCP fp8 formats, whose finite codes
+// 0x00-0x77 (e4m3) / 0x00-0x7b (e5m2) mean exactly what reng-fp8's codes mean.
+//
+// Block = 2 x 2 waves; a wave owns WM x WN tiles of 32 x 32, so the block tile
+// is BM = 64 WM by BN = 64 WN. A pipeline stage covers BK = 64 KS codes of k.
+// Each stage's operand rows are copied global -> LDS by the waves'
+// global_load_lds_dwordx4 (1 KB per instruction, no VGPR staging) into an
+// S-slot ring; a row's 16-byte chunks are stored XOR-swizzled (swz) so that
+// the 32-byte fragment reads (two ds_read_b128 per operand tile) are free of
+// bank conflicts. One barrier per stage: before it a wave waits only for its
+// own copies of the next stage (s_waitcnt vmcnt with the later stages still in
+// flight); after it the wave issues the copy of stage t + S into the slot
+// stage t used and reads the next stage's first fragments, interleaved with
+// the second half of the current stage's MFMAs.
+//
+// Tiles are spread over the 8 XCDs so that the blocks resident on one XCD at a
+// time hold consecutive tiles, m fastest: they share the weight rows
+// b[n0:n0+BN] through that XCD's L2. The output goes out as 8-byte stores of
+// four consecutive n (the MFMA computes D = B A^T, so a lane holds four
+// consecutive output columns of one row).
+#include <type_traits>
+
+#include "common.h"
+#include "gemm.h"
+
+namespace reng {
+
+namespace fp8gemm {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int FK = 64;     // codes of k per MFMA k-step
+constexpr int XCDS = 8;    // MI355X: 8 XCDs, workgroups dispatched round-robin over them
+
+// Block tile BM x BN (2 x 2 waves of WM x WN MFMA tiles), KS k-steps (64 codes
+// each) per pipeline stage.
+template <int WM, int WN, int KS>
+struct Fp8Tile {
+    static constexpr int BM = 64 * WM, BN = 64 * WN, BK = FK * KS;
+    static constexpr int CH = BK / 16;                 // 16-byte chunks per LDS row
+    static constexpr int ROWS = 1024 / BK;             // rows per 1 KB copy
+    static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE = A_BYTES + B_BYTES;
+    static constexpr int LA = BM / 4 / ROWS, LB = BN / 4 / ROWS;   // copies per wave per stage
+    static constexpr int LOADS = LA + LB;
+};
+
+// Slot permutation of an LDS row of CH 16-byte chunks: chunk c of tile row r
+// sits in slot c ^ swz(r). A fragment read takes 32 consecutive rows at one
+// chunk; with these permutations any 8 consecutive rows use 8 distinct slots
+// modulo 128 bytes and any 16 use 16 distinct slots modulo 256 bytes, so the
+// ds_read_b128 phases are free of bank conflicts for 32 or 64 four-byte banks.
+// swz depends on the low five bits of r only: the reader knows its row as
+// (32-row tile base) + lane % 32.
+template <int CH>
+__device__ __forceinline__ uint32_t swz(uint32_t r) {
+    if constexpr (CH == 4) return ((r >> 1) ^ (r >> 3)) & 3;
+    else return (r ^ ((r >> 3) & 3)) & 7;
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | (7 << 4) | (0xf << 8) | ((N >> 4) << 14));
+}
+
+// One global_load_lds_dwordx4: 16 bytes per lane from
+// g into LDS at l + 16 * lane (l is wave-uniform). A __device__ function
+// rather than code in the kernel's lambdas, whose host-side instantiation
+// cannot form the LDS address-space cast.
+__device__ __forceinline__ void copy16_to_lds(const uint8_t *g, uint8_t *l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
+}
+
+// A workgroup barrier that orders LDS traffic for the compiler (the memory
+// clobbers) without the vmcnt(0) that __syncthreads' fence would add.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Scheduling pattern for one region of the stage: NM MFMAs, with NDS LDS
+// reads and NVM vector-memory instructions spread evenly between them, so the
+// MFMA pipe keeps receiving work while the wave issues its copies and
+// fragment reads (a wave issues in order, one wave per SIMD).
+template <int NM, int NDS, int NVM, int I = 0>
+__device__ __forceinline__ void interleave() {
+    if constexpr (I < NM) {
+        constexpr int ds = (NDS * (I + 1)) / NM - (NDS * I) / NM;
+        constexpr int vm = (NVM * (I + 1)) / NM - (NVM * I) / NM;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        if constexpr (ds > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds, 0);   // DS read
+        if constexpr (vm > 0) __builtin_amdgcn_sched_group_barrier(0x060, vm, 0);   // VMEM
+        interleave<NM, NDS, NVM, I + 1>();
+    }
+}
+
+template <int FA, int FB, int WM, int WN, int KS, int S>
+__global__ __launch_bounds__(256) void gemm_fp8_mfma(const uint8_t *__restrict__ a,
+                                                     const float *__restrict__ sa, uint32_t nsa,
+                                                     const uint8_t *__restrict__ b,
+                                                     const float *__restrict__ sb, uint32_t nsb,
+                                                     uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+                                                     uint32_t tiles, uint16_t *__restrict__ out, uint32_t vec_out) {
+    using T = Fp8Tile<WM, WN, KS>;
+    constexpr int BM = T::BM, BN = T::BN, BK = T::BK, CH = T::CH;
+    static_assert(S >= 2, "at least double-buffered");
+    static_assert((S - 1) * T::LOADS < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * T::STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: keeps LDS bases scalar
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // Tile of this block: the XCD (blockIdx % 8) takes a contiguous run.
+    const uint32_t x = blockIdx.x % XCDS, l = blockIdx.x / XCDS;
+    const uint32_t per = tiles / XCDS, rem = tiles % XCDS;
+    const uint32_t tile = x * per + (x < rem ? x : rem) + l;
+    const uint32_t m0 = (tile % tiles_m) * BM, n0 = (tile / tiles_m) * BN;
+    const uint32_t n = K / BK;   // stages
+
+    // Copy sources: lane l of a copy brings tile row r = base + l / CH and the
+    // chunk that lands in slot l % CH of that row, i.e. chunk
+    // (l % CH) ^ swz(r). Rows past M / N are clamped (never stored).
+    const uint8_t *ga[T::LA];
+    const uint8_t *gb[T::LB];
+#pragma unroll
+    for (int q = 0; q < T::LA; ++q) {
+        const uint32_t tr = wave * (BM / 4) + q * T::ROWS + lane / CH;
+        uint32_t r = m0 + tr;
+        r = r < M ? r : M - 1;
+        ga[q] = a + (size_t)r * K + (((lane % CH) ^ swz<CH>(tr)) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < T::LB; ++q) {
+        const uint32_t tr = wave * (BN / 4) + q * T::ROWS + lane / CH;
+        uint32_t r = n0 + tr;
+        r = r < N ? r : N - 1;
+        gb[q] = b + (size_t)r * K + (((lane % CH) ^ swz<CH>(tr)) * 16);
+    }
+    auto issue = [&](uint32_t step, int slot) {
+        uint8_t *base = lds + slot * T::STAGE;
+        const size_t ko = (size_t)step * BK;
+#pragma unroll
+        for (int q = 0; q < T::LA; ++q) copy16_to_lds(ga[q] + ko, base + (wave * (BM / 4) + q * T::ROWS) * BK);
+#pragma unroll
+        for (int q = 0; q < T::LB; ++q)
+            copy16_to_lds(gb[q] + ko, base + T::A_BYTES + (wave * (BN / 4) + q * T::ROWS) * BK);
+    };
+    auto clampi = [&](uint32_t i) { return i < n ? i : n - 1; };
+
+    // Fragment of a 32-row tile at k-step ks: lane l holds row l % 32 and the
+    // 32 codes of k half l / 32, chunks 4 ks + 2h and 4 ks + 2h + 1 of the row.
+    const uint32_t rl = lane & 31, h = lane >> 5, sw = swz<CH>(rl);
+    auto read_frags = [&](int slot, int ks, i32x8 (&fa)[WM], i32x8 (&fb)[WN]) {
+        const uint8_t *base = lds + slot * T::STAGE;
+        const uint32_t o0 = ((4 * ks + 2 * h) ^ sw) * 16, o1 = ((4 * ks + 2 * h + 1) ^ sw) * 16;
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const uint8_t *p = base + (wm * (BM / 2) + i * 32 + rl) * BK;
+            const u32x4 x0 = *reinterpret_cast<const u32x4 *>(p + o0);
+            const u32x4 x1 = *reinterpret_cast<const u32x4 *>(p + o1);
+            fa[i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        }
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const uint8_t *p = base + T::A_BYTES + (wn * (BN / 2) + j * 32 + rl) * BK;
+            const u32x4 x0 = *reinterpret_cast<const u32x4 *>(p + o0);
+            const u32x4 x1 = *reinterpret_cast<const u32x4 *>(p + o1);
+            fb[j] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        }
+    };
+
+    f32x16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    auto mfma_rows = [&](int i0, int i1, const i32x8 (&fa)[WM], const i32x8 (&fb)[WN]) {
+#pragma unroll
+        for (int i = i0; i < i1; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], FB, FA, 0, 0,
+                                                                            0, 0);
+    };
+
+    // Prologue: stages 0 .. S-1 in flight (indices clamped to the last step, so
+    // every wave issues the same number of copies), then the first fragments.
+#pragma unroll
+    for (int s = 0; s < S; ++s) issue(clampi(s), s);
+    wait_vmcnt<(S - 1) * T::LOADS>();
+    lds_barrier();
+    i32x8 fa[2][WM], fb[2][WN];
+    read_frags(0, 0, fa[0], fb[0]);
+
+    // One k-step on the fragment set CUR while the next k-step's fragments go
+    // into the other set. The last k-step of a stage splits its MFMAs around
+    // the barrier that publishes stage t + 1. Every fragment of stage t is in
+    // registers by then (the first half's MFMAs waited for them), so after the
+    // barrier the copy of stage t + S goes into stage t's slot.
+    auto kstep = [&](auto cur_c, auto ks_c, uint32_t t) {
+        constexpr int CUR = decltype(cur_c)::value, NXT = CUR ^ 1, KSI = decltype(ks_c)::value;
+        if constexpr (KSI + 1 < KS) {
+            read_frags((int)(t % S), KSI + 1, fa[NXT], fb[NXT]);
+            mfma_rows(0, WM, fa[CUR], fb[CUR]);
+            interleave<WM * WN, 2 * (WM + WN), 0>();
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            mfma_rows(0, WM / 2, fa[CUR], fb[CUR]);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<(S - 2) * T::LOADS>();
+            lds_barrier();
+            issue(clampi(t + S), (int)(t % S));
+            read_frags((int)((t + 1) % S), 0, fa[NXT], fb[NXT]);
+            mfma_rows(WM / 2, WM, fa[CUR], fb[CUR]);
+            interleave<WM / 2 * WN, 2 * (WM + WN), T::LOADS>();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // Stage t's k-steps use fragment sets (t * KS + ks) & 1.
+    auto stage = [&](auto par_c, uint32_t t) {
+        constexpr int P = decltype(par_c)::value;
+        kstep(std::integral_constant<int, (P * KS) & 1>{}, std::integral_constant<int, 0>{}, t);
+        if constexpr (KS > 1)
+            kstep(std::integral_constant<int, (P * KS + 1) & 1>{}, std::integral_constant<int, 1>{}, t);
+    };
+    static_assert(KS == 1 || KS == 2, "one or two k-steps per stage");
+    uint32_t t = 0;
+    for (; t + 1 < n; t += 2) {
+        stage(std::integral_constant<int, 0>{}, t);
+        stage(std::integral_constant<int, 1>{}, t + 1);
+    }
+    if (t < n) stage(std::integral_constant<int, 0>{}, t);
+    wait_vmcnt<0>();   // the clamped surplus copies land before LDS is released
+    (void)BK;
+
+    // acc[i][j] is D = B A^T of a 32 x 32 tile: lane l holds column
+    // m = l % 32 (activation row) and rows n = 8 (e / 4) + 4 (l / 32) + e % 4,
+    // so each group of four e is four consecutive outputs of row m: one 8-byte
+    // store.
+    auto store = [&](const f32x16 (&v)[WM][WN]) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const uint32_t m = m0 + wm * (BM / 2) + i * 32 + rl;
+            if (m >= M) continue;
+            const float sam = nsa == 0 ? 1.0f : (nsa == 1 ? sa[0] : sa[m]);
+            uint16_t *orow = out + (size_t)m * N;
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const uint32_t nb = n0 + wn * (BN / 2) + j * 32 + 8 * g + 4 * h;
+                    float o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t nn = nb + e < N ? nb + e : N - 1;
+                        const float sbn = nsb == 0 ? 1.0f : (nsb == 1 ? sb[0] : sb[nn]);
+                        o[e] = v[i][j][4 * g + e] * sam * sbn;
+                    }
+                    if (vec_out && nb + 3 < N) {
+                        const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
+                        const uint32_t hi = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
+                        *reinterpret_cast<u32x2 *>(orow + nb) = u32x2{lo, hi};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (nb + e < N) orow[nb + e] = (uint16_t)f32_to_bf16_bits(o[e]);
+                    }
+                }
+        }
+    };
+    store(acc);
+}
+
+struct Fp8Args {
+    const uint8_t *a;
+    int fa;
+    const float *sa;
+    uint32_t nsa;
+    const uint8_t *b;
+    int fb;
+    const float *sb;
+    uint32_t nsb;
+    uint32_t M, N, K;
+    uint16_t *out;
+};
+
+// One launch of the (WM, WN, KS, S) kernel.
+template <int WM, int WN, int KS, int S>
+int launch_fp8_cfg(const Fp8Args &g, hipStream_t st) {
+    using T = Fp8Tile<WM, WN, KS>;
+    const uint32_t tiles_m = (g.M + T::BM - 1) / T::BM, tiles_n = (g.N + T::BN - 1) / T::BN;
+    const uint32_t tiles = tiles_m * tiles_n;
+    // 8-byte output stores need every row start 8-byte aligned.
+    const uint32_t vec_out = g.N % 4 == 0 && reinterpret_cast<uintptr_t>(g.out) % 8 == 0;
+#define RENG_FP8_LAUNCH(A, B)                                                                                \
+    hipLaunchKernelGGL((gemm_fp8_mfma<A, B, WM, WN, KS, S>), dim3(tiles), dim3(256), 0, st, g.a, g.sa, g.nsa, \
+                       g.b, g.sb, g.nsb, g.M, g.N, g.K, tiles_m, tiles, g.out, vec_out)
+    if (g.fa == RENG_HIP_E4M3 && g.fb == RENG_HIP_E4M3) RENG_FP8_LAUNCH(0, 0);
+    else if (g.fa == RENG_HIP_E4M3) RENG_FP8_LAUNCH(0, 1);
+    else if (g.fb == RENG_HIP_E4M3) RENG_FP8_LAUNCH(1, 0);
+    else RENG_FP8_LAUNCH(1, 1);
+#undef RENG_FP8_LAUNCH
+    return check_launch("gemm_fp8_mfma");
+}
+
+}  // namespace fp8gemm
+
+int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, const uint8_t *b, int fb,
+                    const float *sb, uint32_t nsb, uint32_t M, uint32_t N, uint32_t K, uint16_t *out,
+                    hipStream_t st) {
+    using namespace fp8gemm;
+    const Fp8Args g{a, fa, sa, nsa, b, fb, sb, nsb, M, N, K, out};
+    // Tile choice by how many tiles each size gives for the chip (measured on
+    // the M = 1024 prefill shapes): the largest tile that still fills every
+    // CU; 256 x 128 for long K; 64 x 64 for small outputs.
+    const uint64_t cus = (uint64_t)device_props().cus;
+    const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
+    const uint64_t t128 = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+    if (t256 >= cus) return launch_fp8_cfg<4, 4, 2, 2>(g, st);
+    if (t128 >= cus) return K > 8192 ? launch_fp8_cfg<4, 2, 2, 3>(g, st) : launch_fp8_cfg<2, 2, 2, 2>(g, st);
+    if (K > 8192 && 2 * t128 >= cus) return launch_fp8_cfg<4, 2, 2, 3>(g, st);
+    return launch_fp8_cfg<1, 1, 2, 4>(g, st);
+}
+
+}  // namespace reng

@@ -168,7 +168,7 @@ def check_fp8(R, rng, M, N, K, fa, fb, act="pcs", nsb="N", sample_cols=None):
     else:
         b_scale = np.repeat(sb, K)
     b_deq = (O.decode_array(qw.codes, fb) * b_scale).astype(np.float32)
-    if sample_cols:
+    if sample_cols and sample_cols < N:
         idx = np.unique(np.concatenate([rng.choice(N, sample_cols, replace=False), [0, N - 1]]))
         want = O.gemm_cols(a_deq, b_deq, M, K, idx, threads=16).reshape(M, idx.size)
         got = out[:, idx]
@@ -185,6 +185,15 @@ def test_fp8_gemm_formats_and_scale_forms(R, fa, fb):
     rng = np.random.default_rng(113 + 2 * fa + fb)
     for act, nsb in (("pcs", "N"), ("unit", "N"), ("pcs", "1"), ("unit", "0")):
         check_fp8(R, rng, 160, 200, 384, fa, fb, act, nsb)
+
+
+# Ragged edges on each tile size the launcher picks (256 x 256, 128 x 128,
+# 256 x 128 for long K, 64 x 64): M and N off the tile grid, N % 4 != 0 (the
+# scalar output path) and N % 4 == 0 with a partial last tile.
+@pytest.mark.parametrize("M,N,K", [(1000, 16390, 256), (1000, 4100, 384), (520, 8300, 8320), (100, 70, 128)])
+def test_fp8_gemm_ragged_tiles(R, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    check_fp8(R, rng, M, N, K, E4M3, E4M3, sample_cols=160)
 
 
 @pytest.mark.parametrize("shape", [(5120, 5120), (1024, 5120), (27648, 5120), (5120, 27648)])
