@@ -9,13 +9,11 @@ namespace reng {
 
 int launch_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                  uint32_t N, uint32_t K, int format, uint16_t *y, hipStream_t st);
+// 4 < M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
+int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
+                       uint32_t K, int format, uint16_t *y, hipStream_t st);
 int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, const uint8_t *b,
                     int fb, const float *sb, uint32_t nsb, uint32_t M, uint32_t N, uint32_t K,
                     uint16_t *out, hipStream_t st);
-
-// Grow-only f32 scratch for k-split partial sums, one per (device, stream):
-// calls on one stream are ordered and share it. Sets *rc and returns null on
-// failure.
-float *split_workspace(size_t floats, hipStream_t st, int *rc);
 
 }  // namespace reng

@@ -3,11 +3,10 @@
 // 1. gemv_w8a16     (M <= 4): y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]).
 //    Streams the codes once with 16-byte loads, decodes in registers
 //    (v_cvt_pk_f32_fp8 / _bf8), f32 FMA, one wave per output row.
-// 2. skinny_w8a16   (4 < M <= 64): the same product on bf16 MFMA
-//    (v_mfma_f32_16x16x32_bf16): codes decoded to bf16 in registers
-//    (v_cvt_scalef32_pk_bf16_fp8, exact: bf16 holds every e4m3 / e5m2 value),
-//    activations as the B operand; the four waves of a block split K and meet
-//    in LDS.
+// 2. 4 < M <= 16: the same product on bf16 MFMA, register-streaming waves
+//    (skinny.hip).
+// 3. 16 < M <= 64: skinny_w8a16 below, bf16 MFMA with the activation tile
+//    shared by the block's waves through LDS.
 // (The fp8 x fp8 product of gemm_fp8_scaled is in gemm_fp8.hip.)
 //
 // The reference semantics are gemm_cpu over Quantized::dequantize
@@ -325,100 +324,6 @@ __global__ __launch_bounds__(256) void skinny_w8a16(const uint16_t *__restrict__
     }
 }
 
-// M <= 16: independent waves, no LDS and no barrier. A wave owns AF fragments
-// (16 * AF output rows); per 128-code step it reads its codes (prefetched two
-// steps ahead) and the step's 16-column activation fragment (64 bytes per
-// lane, from L2, one step ahead), and issues AF * 4 MFMAs. Split-K over
-// blockIdx.y as in skinny_w8a16.
-template <int F, int AF>
-__global__ __launch_bounds__(256) void skinny_small(const uint16_t *__restrict__ x,
-                                                    const uint8_t *__restrict__ codes,
-                                                    const float *__restrict__ scales, uint32_t M,
-                                                    uint32_t N, uint32_t K, uint32_t steps_per_split,
-                                                    uint16_t *__restrict__ y, float *__restrict__ part) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r16 = lane & 15, g4 = lane >> 4;
-    const uint32_t n0 = (blockIdx.x * 4 + wave) * (16 * AF);
-    if (n0 >= N) return;
-    const uint32_t steps = K / SK_STEP;
-    const uint32_t s0 = blockIdx.y * steps_per_split;
-    const uint32_t s1 = s0 + steps_per_split < steps ? s0 + steps_per_split : steps;
-    const bool mrow = (uint32_t)r16 < M;
-    const uint16_t *xrow = x + (size_t)(mrow ? r16 : 0) * K + 32 * g4;
-
-    auto load_w = [&](uint32_t st, u32x4 (&q)[AF][2]) {
-#pragma unroll
-        for (int f = 0; f < AF; ++f) {
-            uint32_t n = n0 + f * 16 + r16;
-            n = n < N ? n : N - 1;
-            const u32x4 *wp = reinterpret_cast<const u32x4 *>(codes + (size_t)n * K + st * SK_STEP + 32 * g4);
-            q[f][0] = __builtin_nontemporal_load(wp);
-            q[f][1] = __builtin_nontemporal_load(wp + 1);
-        }
-    };
-    auto load_b = [&](uint32_t st, u32x4 (&b)[4]) {
-        const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow + st * SK_STEP);
-#pragma unroll
-        for (int sl = 0; sl < 4; ++sl) b[sl] = mrow ? xp[sl] : u32x4{0u, 0u, 0u, 0u};
-    };
-
-    f32x4 acc[AF];
-#pragma unroll
-    for (int f = 0; f < AF; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-    u32x4 q0[AF][2], q1[AF][2], q2[AF][2], b0[4], b1[4];
-    load_w(s0, q0);
-    load_b(s0, b0);
-    load_w(s0 + 1 < s1 ? s0 + 1 : s1 - 1, q1);
-    for (uint32_t st = s0; st < s1; ++st) {
-        // Unconditional prefetches (clamped to the split's last step): no branch,
-        // so each use waits only for the loads issued before it.
-        load_w(st + 2 < s1 ? st + 2 : s1 - 1, q2);
-        load_b(st + 1 < s1 ? st + 1 : s1 - 1, b1);
-#pragma unroll
-        for (int f = 0; f < AF; ++f) {
-            const uint32_t d[8] = {q0[f][0].x, q0[f][0].y, q0[f][0].z, q0[f][0].w,
-                                   q0[f][1].x, q0[f][1].y, q0[f][1].z, q0[f][1].w};
-#pragma unroll
-            for (int sl = 0; sl < 4; ++sl) {
-                const bf16x2 p0 = dec2_bf16<F>(d[2 * sl], false), p1 = dec2_bf16<F>(d[2 * sl], true);
-                const bf16x2 p2 = dec2_bf16<F>(d[2 * sl + 1], false), p3 = dec2_bf16<F>(d[2 * sl + 1], true);
-                const bf16x8 a = bf16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-                acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, b0[sl]), acc[f], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int f = 0; f < AF; ++f) {
-            q0[f][0] = q1[f][0];
-            q0[f][1] = q1[f][1];
-            q1[f][0] = q2[f][0];
-            q1[f][1] = q2[f][1];
-        }
-#pragma unroll
-        for (int sl = 0; sl < 4; ++sl) b0[sl] = b1[sl];
-    }
-#pragma unroll
-    for (int f = 0; f < AF; ++f) {
-        const uint32_t nb = n0 + f * 16 + 4 * g4;
-        if (!mrow) continue;
-        const uint32_t m = r16;
-        if (part) {
-            float *pp = part + ((size_t)blockIdx.y * M + m) * N;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (nb + e < N) pp[nb + e] = acc[f][e];
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t n = nb + e;
-                if (n < N) {
-                    const float sc = scales ? scales[n] : 1.0f;
-                    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[f][e] * sc);
-                }
-            }
-        }
-    }
-}
-
 // y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the split-K partials summed in order.
 __global__ void skinny_epilogue(const float *__restrict__ part, uint32_t splits, uint32_t M, uint32_t N,
                                 const float *__restrict__ scales, uint16_t *__restrict__ y) {
@@ -512,38 +417,6 @@ int launch_skinny_t(const uint16_t *x, const uint8_t *codes, const float *scales
     return rc;
 }
 
-// M <= 16: independent waves of 64 rows, split-K until there are ~3 waves per CU.
-template <int F>
-int launch_skinny_small(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
-                        uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
-    constexpr int AF = 4;
-    const uint32_t wave_tiles = (N + 16 * AF - 1) / (16 * AF);
-    const SplitPlan p = plan_splits(wave_tiles, K / SK_STEP, 3u * (uint32_t)device_props().cus);
-    int rc = RENG_HIP_OK;
-    float *part = p.splits > 1 ? split_workspace((size_t)p.splits * M * N, st, &rc) : nullptr;
-    if (rc) return rc;
-    hipLaunchKernelGGL((skinny_small<F, AF>), dim3((wave_tiles + 3) / 4, p.splits), dim3(256), 0, st, x, codes,
-                       scales, M, N, K, p.steps_per_split, y, part);
-    rc = check_launch("skinny_small");
-    if (rc == RENG_HIP_OK && part) rc = launch_epilogue(part, p.splits, M, N, scales, y, st);
-    return rc;
-}
-
-template <int F>
-int launch_skinny(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
-                  uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
-    if (M <= 16) return launch_skinny_small<F>(x, codes, scales, M, N, K, y, st);
-    const bool wide = N >= 1024;
-    switch ((M + 15) / 16) {
-        case 2: return wide ? launch_skinny_t<F, 2, 2>(x, codes, scales, M, N, K, y, st)
-                            : launch_skinny_t<F, 2, 1>(x, codes, scales, M, N, K, y, st);
-        case 3: return wide ? launch_skinny_t<F, 3, 2>(x, codes, scales, M, N, K, y, st)
-                            : launch_skinny_t<F, 3, 1>(x, codes, scales, M, N, K, y, st);
-        default: return wide ? launch_skinny_t<F, 4, 2>(x, codes, scales, M, N, K, y, st)
-                             : launch_skinny_t<F, 4, 1>(x, codes, scales, M, N, K, y, st);
-    }
-}
-
 template <int F>
 int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
@@ -596,7 +469,22 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     // Larger M: tiles of up to 64 activation rows on the MFMA kernel.
     for (uint32_t mb = 0; mb < M; mb += 64) {
         const uint32_t mt = M - mb < 64 ? M - mb : 64;
-        const int rc = launch_skinny<F>(x + (size_t)mb * K, codes, scales, mt, N, K, y + (size_t)mb * N, st);
+        int rc;
+        if (mt <= 16) {
+            rc = launch_skinny_mfma(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st);
+        } else {
+            const bool wide = N >= 1024;
+            const uint16_t *xb = x + (size_t)mb * K;
+            uint16_t *yb = y + (size_t)mb * N;
+            switch ((mt + 15) / 16) {
+                case 2: rc = wide ? launch_skinny_t<F, 2, 2>(xb, codes, scales, mt, N, K, yb, st)
+                                  : launch_skinny_t<F, 2, 1>(xb, codes, scales, mt, N, K, yb, st); break;
+                case 3: rc = wide ? launch_skinny_t<F, 3, 2>(xb, codes, scales, mt, N, K, yb, st)
+                                  : launch_skinny_t<F, 3, 1>(xb, codes, scales, mt, N, K, yb, st); break;
+                default: rc = wide ? launch_skinny_t<F, 4, 2>(xb, codes, scales, mt, N, K, yb, st)
+                                   : launch_skinny_t<F, 4, 1>(xb, codes, scales, mt, N, K, yb, st); break;
+            }
+        }
         if (rc) return rc;
     }
     return RENG_HIP_OK;
