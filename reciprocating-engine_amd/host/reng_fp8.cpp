@@ -166,12 +166,13 @@ std::vector<uint16_t> Quantized::dequantize_bf16() const {
 
 // ------------------------------------------------------------ errors
 
-static std::vector<RowError> errors_impl(const std::vector<uint16_t> &w, const Quantized &q, size_t max_rows) {
-    if (w.size() != q.rows * q.cols) throw std::invalid_argument("weight length against the shape");
+static std::vector<RowError> errors_impl(const uint16_t *w, size_t len, const Quantized &q, size_t max_rows) {
+    if (len != q.rows * q.cols) throw std::invalid_argument("weight length against the shape");
+    if (q.rows == 0) return {};
     const size_t n = max_rows == 0 ? q.rows : std::min(max_rows, q.rows);
     const size_t step = (q.rows + n - 1) / n;
     const size_t k = (q.rows + step - 1) / step;
-    DevBuf dw(w.data(), w.size() * 2), dc(q.codes.data(), q.codes.size()), ds(q.scales.data(), q.scales.size() * 4);
+    DevBuf dw(w, len * 2), dc(q.codes.data(), q.codes.size()), ds(q.scales.data(), q.scales.size() * 4);
     DevBuf dmean(k * 4), dmax(k * 4);
     check(reng_hip_row_errors(dw.as<uint16_t>(), dc.as<uint8_t>(), ds.as<float>(), q.rows, q.cols, (int)q.format,
                               max_rows, dmean.as<float>(), dmax.as<float>(), nullptr));
@@ -183,24 +184,38 @@ static std::vector<RowError> errors_impl(const std::vector<uint16_t> &w, const Q
     return out;
 }
 
-std::vector<RowError> row_errors(const std::vector<uint16_t> &w, const Quantized &q) { return errors_impl(w, q, 0); }
+std::vector<RowError> row_errors(const uint16_t *w, size_t len, const Quantized &q) {
+    return errors_impl(w, len, q, 0);
+}
+
+std::vector<RowError> sample_row_errors(const uint16_t *w, size_t len, const Quantized &q, size_t max_rows) {
+    if (len != q.rows * q.cols) throw std::invalid_argument("weight length against the shape");
+    if (max_rows == 0) throw std::invalid_argument("max_rows must be positive");
+    return errors_impl(w, len, q, max_rows);
+}
+
+std::vector<RowError> row_errors(const std::vector<uint16_t> &w, const Quantized &q) {
+    return row_errors(w.data(), w.size(), q);
+}
 
 std::vector<RowError> sample_row_errors(const std::vector<uint16_t> &w, const Quantized &q, size_t max_rows) {
-    if (w.size() != q.rows * q.cols) throw std::invalid_argument("weight length against the shape");
-    if (max_rows == 0) throw std::invalid_argument("max_rows must be positive");
-    return errors_impl(w, q, max_rows);
+    return sample_row_errors(w.data(), w.size(), q, max_rows);
 }
 
 // ------------------------------------------------------------ quantize
 
-std::vector<float> row_absmax(const std::vector<uint16_t> &w, size_t rows, size_t cols) {
-    if (w.size() != rows * cols) throw std::invalid_argument("weight length against the shape");
+std::vector<float> row_absmax(const uint16_t *w, size_t len, size_t rows, size_t cols) {
+    if (len != rows * cols) throw std::invalid_argument("weight length against the shape");
     std::vector<float> out(rows);
     if (rows == 0 || cols == 0) return out;
-    DevBuf dw(w.data(), w.size() * 2), dout(rows * 4);
+    DevBuf dw(w, len * 2), dout(rows * 4);
     check(reng_hip_row_absmax(dw.as<void>(), RENG_HIP_BF16, rows, cols, cols, dout.as<float>(), nullptr));
     dout.to_host(out.data(), rows * 4);
     return out;
+}
+
+std::vector<float> row_absmax(const std::vector<uint16_t> &w, size_t rows, size_t cols) {
+    return row_absmax(w.data(), w.size(), rows, cols);
 }
 
 uint32_t choose_exp_bias(float absmax, Fp8Format fmt) { return reng_hip_choose_exp_bias(absmax, (int)fmt); }

@@ -79,10 +79,15 @@ struct RowError {
 std::vector<RowError> row_errors(const std::vector<uint16_t> &w, const Quantized &q);
 std::vector<RowError> sample_row_errors(const std::vector<uint16_t> &w, const Quantized &q,
                                         size_t max_rows);
+// The same over a borrowed span (an mmap'd checkpoint view).
+std::vector<RowError> row_errors(const uint16_t *w, size_t len, const Quantized &q);
+std::vector<RowError> sample_row_errors(const uint16_t *w, size_t len, const Quantized &q,
+                                        size_t max_rows);
 
 // ------------------------------------------------------------ quantize (lib.rs:433-563)
 
 std::vector<float> row_absmax(const std::vector<uint16_t> &w, size_t rows, size_t cols);
+std::vector<float> row_absmax(const uint16_t *w, size_t len, size_t rows, size_t cols);
 uint32_t choose_exp_bias(float absmax, Fp8Format fmt);
 
 constexpr float DEFAULT_BACKOFF = 1.0f;
