@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../../oracle/fp8_oracle.h"
+#include "../../reciprocating-engine_amd/host/fp8_probe.hpp"
 #include "../../reciprocating-engine_amd/host/reng_model.hpp"
 
 using namespace reng_model;
@@ -437,6 +438,87 @@ void quantize_fp8_matches_the_oracle_on_every_matrix() {
     }
 }
 
+// ------------------------------------------------------------------ the probe (fp8_probe.rs)
+
+// The probe's host references: the closed-form decode against the oracle
+// for every code, and the nearest-value encode against the oracle's encoder
+// over every bf16 pattern and the reference's known answers.
+void the_probe_host_references_agree_with_the_oracle() {
+    for (Fp8Format f : {Fp8Format::E4M3, Fp8Format::E5M2}) {
+        for (int c = 0; c < 256; ++c) {
+            const float a = reng_probe::host_decode((uint8_t)c, f), b = orc_decode((uint8_t)c, (int)f);
+            expect(std::memcmp(&a, &b, 4) == 0 || (std::isnan(a) && std::isnan(b)), "decode " + std::to_string(c));
+        }
+        for (uint32_t h = 0; h < 65536; ++h) {
+            const float x = reng_fp8::bf16_to_f32((uint16_t)h);
+            const uint8_t got = reng_probe::host_encode(x, f), want = orc_encode(x, (int)f);
+            if (std::isnan(x)) {
+                expect((got & 0x7f) == 0x7f && (want & 0x7f) == 0x7f, "NaN");
+            } else {
+                expect(got == want, "encode bf16 " + std::to_string(h));
+            }
+        }
+    }
+    const std::pair<float, uint8_t> kat[] = {{1.375f, 0x3b}, {-3.3f, 0xc5}, {100.0f, 0x6c}, {0.01f, 0x05},
+                                             {250.0f, 0x77}, {300.0f, 0x77}, {0.001f, 0x01}, {1e-9f, 0x00},
+                                             {17.0f, 0x58}, {1.0625f, 0x38}, {1.1875f, 0x3a}};
+    for (const auto &k : kat) expect(reng_probe::host_encode(k.first, Fp8Format::E4M3) == k.second, "KAT");
+}
+
+void the_probe_inputs_are_the_reference_ones() {
+    const auto w = reng_probe::weights(2, 1000);
+    // i = 0 is an outlier channel (x 12): ((0 % 65536) / 65536 - 0.5) * 0.08 * 12.
+    expect(w[0] == reng_fp8::f32_to_bf16(-0.04f * 12.0f), "weights[0]");
+    const float x1 = ((float)((1ull * 2654435761ull) % 65536) / 65536.0f - 0.5f) * 0.08f;
+    expect(w[1] == reng_fp8::f32_to_bf16(x1), "weights[1]");
+    expect(w[977] == reng_fp8::f32_to_bf16(((float)((977ull * 2654435761ull) % 65536) / 65536.0f - 0.5f) * 0.08f * 12.0f),
+           "weights[977]");
+    const auto a = reng_probe::activations(3);
+    expect(a[0] == -1000.0f / 700.0f && a[1] == ((float)(7919 % 2003) - 1000.0f) / 700.0f, "activations");
+    expect(reng_probe::rel_l2({1.0f, 2.0f}, {1.0f, 2.0f}) == 0.0f, "rel_l2 0");
+    const auto c = reng_probe::gemm_cpu({1, 2, 3, 4}, {1, 0, 0, 1, 1, 1}, 2, 2, 3);
+    expect((c == std::vector<float>{1, 2, 3, 3, 4, 7}), "gemm_cpu");
+}
+
+// fp8_probe.rs:538-597, the probe's own tests.
+void the_plain_gemm_reference_is_the_dequantized_weight() {
+    const auto w = reng_probe::weights(512, 256);
+    const auto q = reng_fp8::quantize(w, 512, 256, Fp8Format::E4M3, Scaling::HwExpBias);
+    expect(q.exp_bias != reng_fp8::exponent_bias(Fp8Format::E4M3), "a non-default bias");
+    expect(reng_probe::device_values(q) == q.dequantize(), "device values == dequantize");
+}
+
+void a_unit_scaled_operand_is_read_as_its_codes() {
+    const auto af = reng_probe::activations(256);
+    std::vector<uint16_t> a(256);
+    for (size_t i = 0; i < 256; ++i) a[i] = reng_fp8::f32_to_bf16(af[i]);
+    const auto q = reng_fp8::quantize(a, 1, 256, Fp8Format::E4M3, Scaling::Unit);
+    std::vector<float> want(256);
+    for (size_t i = 0; i < 256; ++i) want[i] = reng_probe::host_decode(q.codes[i], Fp8Format::E4M3);
+    expect(reng_probe::device_values(q) == want, "unit operand");
+}
+
+void the_plain_gemm_reference_refuses_a_per_channel_weight() {
+    const auto w = reng_probe::weights(512, 256);
+    const auto q = reng_fp8::quantize(w, 512, 256, Fp8Format::E4M3, Scaling::PerChannel);
+    expect_throws<std::logic_error>([&] { (void)reng_probe::device_values(q); }, "does not see per-channel scales",
+                                    "per-channel refused");
+}
+
+void a_per_channel_reference_would_miss_the_plain_gemm_by_thousands() {
+    const auto w = reng_probe::weights(512, 256);
+    const auto q = reng_fp8::quantize(w, 512, 256, Fp8Format::E4M3, Scaling::PerChannel);
+    const auto af = reng_probe::activations(256);
+    std::vector<uint16_t> a(256);
+    for (size_t i = 0; i < 256; ++i) a[i] = reng_fp8::f32_to_bf16(af[i]);
+    const auto aq = reng_fp8::quantize(a, 1, 256, Fp8Format::E4M3, Scaling::Unit);
+    std::vector<float> read(q.codes.size());
+    for (size_t i = 0; i < read.size(); ++i) read[i] = reng_probe::host_decode(q.codes[i], Fp8Format::E4M3);
+    const auto dev = reng_probe::gemm_cpu(reng_probe::device_values(aq), read, 1, 256, 512);
+    const auto scaled = reng_probe::gemm_cpu(reng_probe::device_values(aq), q.dequantize(), 1, 256, 512);
+    expect(reng_probe::rel_l2(dev, scaled) > 100.0f, "rel_L2 " + std::to_string(reng_probe::rel_l2(dev, scaled)));
+}
+
 struct Test {
     const char *name;
     bool device;
@@ -454,6 +536,14 @@ const Test TESTS[] = {
     {"the_fp8_switch_on_quantizes_the_projections_and_nothing_else", true,
      the_fp8_switch_on_quantizes_the_projections_and_nothing_else},
     {"quantize_fp8_matches_the_oracle_on_every_matrix", true, quantize_fp8_matches_the_oracle_on_every_matrix},
+    {"the_probe_host_references_agree_with_the_oracle", false, the_probe_host_references_agree_with_the_oracle},
+    {"the_probe_inputs_are_the_reference_ones", false, the_probe_inputs_are_the_reference_ones},
+    {"the_plain_gemm_reference_is_the_dequantized_weight", true, the_plain_gemm_reference_is_the_dequantized_weight},
+    {"a_unit_scaled_operand_is_read_as_its_codes", true, a_unit_scaled_operand_is_read_as_its_codes},
+    {"the_plain_gemm_reference_refuses_a_per_channel_weight", true,
+     the_plain_gemm_reference_refuses_a_per_channel_weight},
+    {"a_per_channel_reference_would_miss_the_plain_gemm_by_thousands", true,
+     a_per_channel_reference_would_miss_the_plain_gemm_by_thousands},
 };
 
 }  // namespace
