@@ -5,21 +5,12 @@
 // (crates/reng-model/src/bin/fp8_probe.rs:55-67) with the per-channel scaleB
 // of fp8_gemm_bf16 (crates/reng-synapse/src/fp8.rs:295-331).
 //
-// A block owns 16 NT weight rows; its WPB waves split K between them, so the
-// whole product of the block's rows is one block's work: no partial sums
-// leave the block and there is one launch. Each wave streams its rows' codes
-// and the activation fragments straight into registers (no LDS, no barrier
-// until the end), prefetching P 128-code chunks ahead with unconditional,
-// clamped loads. v_mfma_f32_16x16x32_bf16: the A operand is 16 weight rows
-// x 32 k (codes decoded to bf16 in registers, exact: bf16 holds every e4m3 /
-// e5m2 value), the B operand 32 k x 16 activation rows. Within a 128-code
-// chunk lane l (row l % 16, group g = l / 16) holds the 32 consecutive codes
-// [16 g, 16 g + 16) and [64 + 16 g, 64 + 16 g + 16) of its row (each load
-// instruction reads contiguous 64-byte runs), k-steps 0, 1 take the first
-// piece's halves and 2, 3 the second's; the activation fragment uses the same
-// k assignment (a permutation of k shared by both operands). At the end the waves' accumulators meet in LDS
-// and are added in wave order (deterministic), scaled per row and stored as
-// four consecutive bf16 per lane.
+// The MFMA operand layout wants 16 different weight rows across a wave's
+// lanes, which read straight from memory is 16 rows x 64 bytes per load
+// instruction: that pattern streams HBM at ~4 TB/s on this device against
+// ~5.5 TB/s for 4 rows x 256 bytes. So the codes (and the activation) go
+// through LDS: copied in 4 x 256-byte pieces by global_load_lds and read back
+// transposed (skinny_rows below). One launch, no partial sums in memory.
 #include <type_traits>
 
 #include "common.h"
@@ -35,7 +26,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int CHUNK = 128;   // codes of k per chunk
+constexpr int CHUNK = 128;     // codes of k per chunk
+constexpr int STAGE_K = 256;   // codes of k per pipeline stage (two chunks)
 
 template <int F>
 __device__ __forceinline__ bf16x2 dec2(uint32_t w, bool hi);
@@ -58,144 +50,194 @@ __device__ __forceinline__ bf16x8 dec8(uint32_t w0, uint32_t w1) {
     return bf16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-// fn(integral_constant<I>) for I = B .. E-1, unrolled at compile time.
-template <int B, int E, typename Fn>
-__device__ __forceinline__ void static_for(Fn &&fn) {
-    if constexpr (B < E) {
-        fn(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(fn);
-    }
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | (7 << 4) | (0xf << 8) | ((N >> 4) << 14));
 }
 
-// One chunk of a wave's operands: NT weight tiles (2 x 16 bytes per lane) and
-// MT activation tiles (4 x 16 bytes per lane).
-template <int NT, int MT>
-struct Chunk {
-    u32x4 w[NT][2];
-    u32x4 a[MT][4];
-};
+// One global_load_lds_dwordx4: 16 bytes per lane from g into LDS at
+// l + 16 * lane (l is wave-uniform). A __device__ function because the
+// kernel's lambdas cannot form the LDS address-space cast in their host-side
+// instantiation.
+__device__ __forceinline__ void copy16(const uint8_t *g, uint8_t *l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
+}
 
-template <int F, int MT, int NT, int KW, int NW, int P>
-__global__ __launch_bounds__(64 * KW * NW) void skinny_mfma(const uint16_t *__restrict__ x,
-                                                        const uint8_t *__restrict__ codes,
-                                                        const float *__restrict__ scales, uint32_t M, uint32_t N,
-                                                        uint32_t K, uint16_t *__restrict__ y) {
-    constexpr int TILES = NT * MT;
-    __shared__ __attribute__((aligned(16))) f32x4 red[KW > 1 ? KW : 1][KW > 1 ? NW : 1][KW > 1 ? TILES : 1][64];
+// A block of KW x NW waves owns 16 NT NW weight rows; wave (kw, nw) takes the
+// rows [16 NT nw, +16 NT) of the block over the kw-th of KW equal runs of
+// 128-code chunks of K. A pipeline stage is 256 codes (two chunks; the last
+// stage of a run may hold only one). Each wave streams its stages into a
+// private S-slot LDS ring with global_load_lds, so its loop has no barrier:
+//   weights, per 16-row tile: 4 copies of 4 rows x 256 bytes (contiguous
+//     256-byte runs per row), 16-byte piece p of row r stored in slot p ^ (r % 16);
+//   activation: MA / 2 copies of 2 rows x 512 bytes (256 bf16), 8-element
+//     piece p of row r stored in slot p ^ (r % 16); rows >= M repeat row M - 1.
+// The loop issues only these copies (no loads into registers), so the waits
+// are explicit s_waitcnt vmcnt: stage st + S - 1 is requested before stage st
+// is consumed, and consuming st waits for all but the (S - 1) newer stages.
+// MFMA operands are read back with ds_read_b128 in the v_mfma_f32_16x16x32_bf16
+// layout (the XOR slots make each 16-lane phase hit 16 distinct 16-byte bank
+// groups): lane l takes weight row l % 16, codes [16 g, +16) and [64 + 16 g,
+// +16) of a chunk (g = l / 16; k-steps 0, 1 and 2, 3), decoded to bf16 in
+// registers (exact), and the activation row l % 16 at the same k. At the end
+// the KW partial tiles of a row group meet in LDS and are added in kw order.
+template <int F, int MA, int NT, int KW, int NW, int S>
+__global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__restrict__ x,
+                                                            const uint8_t *__restrict__ codes,
+                                                            const float *__restrict__ scales, uint32_t M,
+                                                            uint32_t N, uint32_t K, uint16_t *__restrict__ y) {
+    constexpr int TILE = 16 * STAGE_K;               // one 16-row tile of a stage, bytes
+    constexpr int WBYTES = NT * TILE, ABYTES = MA * STAGE_K * 2;
+    constexpr int SLOT = WBYTES + ABYTES, RING = S * SLOT;
+    constexpr int CA = MA / 2, C = 4 * NT + CA;      // copies per stage
+    static_assert(S >= 2 && (S - 1) * C < 64, "pipeline depth");
+    constexpr int W = KW * NW;
+    constexpr int RED = KW > 1 ? W * NT * 1024 : 0;
+    constexpr int LDS = W * RING > RED ? W * RING : RED;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
+
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kw = wave / NW, nw = wave % NW;
     const uint32_t r16 = lane & 15, g = lane >> 4;
     const uint32_t n0 = (blockIdx.x * NW + nw) * (16 * NT);
-
-    // This wave's chunks of K: [c0, c1), possibly empty. Waves with the same
-    // kw read the same activation bytes (through L1); waves with the same nw
-    // share rows and are added up at the end.
     const uint32_t chunks = K / CHUNK;
     const uint32_t c0 = kw * chunks / KW, c1 = (kw + 1) * chunks / KW;
+    const uint32_t nst = (c1 - c0 + 1) / 2;
+    uint8_t *ring = lds + wave * RING;
 
-    // Row pointers (clamped: rows past N / M are read but never stored).
-    const uint8_t *wp[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        uint32_t n = n0 + t * 16 + r16;
-        n = n < N ? n : N - 1;
-        wp[t] = codes + (size_t)n * K + 16 * g;
-    }
-    const uint16_t *ap[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        uint32_t m = mt * 16 + r16;
-        m = m < M ? m : M - 1;
-        ap[mt] = x + (size_t)m * K + 16 * g;
-    }
-    auto load = [&](uint32_t c, Chunk<NT, MT> &ch) {
-        const size_t ko = (size_t)c * CHUNK;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const u32x4 *p = reinterpret_cast<const u32x4 *>(wp[t] + ko);
-            ch.w[t][0] = __builtin_nontemporal_load(p);
-            ch.w[t][1] = __builtin_nontemporal_load(p + 4);
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const u32x4 *p = reinterpret_cast<const u32x4 *>(ap[mt] + ko);
-            ch.a[mt][0] = p[0];
-            ch.a[mt][1] = p[1];
-            ch.a[mt][2] = p[8];
-            ch.a[mt][3] = p[9];
-        }
-    };
-
-    f32x4 acc[NT][MT];
+    // Copy sources. Weight copy (t, i), lane j: row rr = 4 i + j / 16 of tile
+    // t, piece p = (j % 16) ^ rr. Activation copy i, lane j: row 2 i + j / 32,
+    // piece p = (j % 32) ^ (row % 16). Pieces in a stage's second chunk step
+    // back one chunk in a one-chunk stage (copied, never read).
+    const uint8_t *wsrc[NT][4];
+    uint32_t whi = 0;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    if (c0 < c1) {
-        // Ring of P chunks in registers; the chunk P - 1 ahead is requested
-        // before the current one is consumed (indices clamped to c1 - 1, so
-        // every load is unconditional and each use waits only for its own).
-        Chunk<NT, MT> ring[P];
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t rr = 4 * i + g, p = r16 ^ rr;
+            uint32_t n = n0 + 16 * t + rr;
+            n = n < N ? n : N - 1;   // rows past N are read but never stored
+            wsrc[t][i] = codes + (size_t)n * K + (size_t)c0 * CHUNK + (p >> 3) * CHUNK + (p & 7) * 16;
+            whi |= (p >> 3) << (4 * t + i);
+        }
+    const uint16_t *asrc[CA];
+    uint32_t ahi = 0;
 #pragma unroll
-        for (int p = 0; p < P - 1; ++p) load(c0 + p < c1 ? c0 + p : c1 - 1, ring[p]);
-        uint32_t c = c0;
-        auto step = [&](auto slot_c) {
-            constexpr int SL = decltype(slot_c)::value;
-            const uint32_t ahead = c + P - 1;
-            load(ahead < c1 ? ahead : c1 - 1, ring[(SL + P - 1) % P]);
-            const Chunk<NT, MT> &ch = ring[SL];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                bf16x8 wa[NT];
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const u32x4 &q = ch.w[t][j >> 1];
-                    wa[t] = (j & 1) ? dec8<F>(q.z, q.w) : dec8<F>(q.x, q.y);
-                }
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const bf16x8 b = __builtin_bit_cast(bf16x8, ch.a[mt][j]);
-#pragma unroll
-                    for (int t = 0; t < NT; ++t)
-                        acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[t], b, acc[t][mt], 0, 0, 0);
-                }
-            }
-            ++c;
-        };
-        // Unrolled by P so the ring slots are compile-time indices.
-        while (c + P <= c1) static_for<0, P>(step);
-        // Tail (fewer than P chunks left): the slots continue in order.
-        static_for<0, P>([&](auto ic) {
-            if (c < c1) step(ic);
-        });
+    for (int i = 0; i < CA; ++i) {
+        const uint32_t row = 2 * i + (lane >> 5), p = (lane & 31) ^ (row & 15);
+        const uint32_t m = row < M ? row : M - 1;
+        asrc[i] = x + (size_t)m * K + (size_t)c0 * CHUNK + (p >> 4) * CHUNK + (p & 15) * 8;
+        ahi |= (p >> 4) << i;
     }
-
-    // Waves of the same rows meet in LDS and are added in kw order; tile i of
-    // the row group is stored by the wave with kw == i % KW.
-    if constexpr (KW > 1) {
+    auto one_chunk = [&](uint32_t st) { return c0 + 2 * st + 1 >= c1; };
+    auto copies = [&](uint32_t st) {
+        const bool half = one_chunk(st);
+        uint8_t *slot = ring + (st % S) * SLOT;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) red[kw][nw][t * MT + mt][lane] = acc[t][mt];
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t back = (half && ((whi >> (4 * t + i)) & 1)) ? CHUNK : 0u;
+                copy16(wsrc[t][i] + (size_t)st * STAGE_K - back, slot + t * TILE + i * 1024);
+            }
+#pragma unroll
+        for (int i = 0; i < CA; ++i) {
+            const uint32_t back = (half && ((ahi >> i) & 1)) ? CHUNK : 0u;
+            copy16(reinterpret_cast<const uint8_t *>(asrc[i] + (size_t)st * STAGE_K - back),
+                   slot + WBYTES + i * 1024);
+        }
+    };
+
+    f32x4 acc[NT][2];   // two accumulators per tile: even and odd k-steps
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Chunk h of a stage: weight pieces 8 h + g, 8 h + 4 + g; activation
+    // elements 128 h + 16 g + 8 (j & 1) + 64 (j >> 1) for k-step j, i.e. piece
+    // 16 h + 2 g + (j & 1) + 8 (j >> 1).
+    const uint32_t am = r16 < M ? r16 : M - 1;
+    auto compute = [&](uint32_t st) {
+        const bool half = one_chunk(st);
+        const uint8_t *slot = ring + (st % S) * SLOT;
+        const uint8_t *arow = slot + WBYTES + am * (STAGE_K * 2);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h == 1 && half) break;
+            u32x4 w[NT][2];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint8_t *tb = slot + t * TILE + r16 * STAGE_K;
+                w[t][0] = *reinterpret_cast<const u32x4 *>(tb + (((8 * h + g) ^ r16) * 16));
+                w[t][1] = *reinterpret_cast<const u32x4 *>(tb + (((8 * h + 4 + g) ^ r16) * 16));
+            }
+            u32x4 a[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t p = 16 * h + 2 * g + (j & 1) + 8 * (j >> 1);
+                a[j] = *reinterpret_cast<const u32x4 *>(arow + ((p ^ (am & 15)) * 16));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bf16x8 b = __builtin_bit_cast(bf16x8, a[j]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const u32x4 &q = w[t][j >> 1];
+                    const bf16x8 wa = (j & 1) ? dec8<F>(q.z, q.w) : dec8<F>(q.x, q.y);
+                    acc[t][j & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, b, acc[t][j & 1], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    if (c0 < c1) {
+#pragma unroll
+        for (int s = 0; s < S - 1; ++s)
+            if ((uint32_t)s < nst) copies(s);
+        for (uint32_t st = 0; st < nst; ++st) {
+            if (st + S - 1 < nst) {
+                copies(st + S - 1);
+                wait_vmcnt<(S - 1) * C>();   // stage st has landed; S - 1 newer stages in flight
+            } else {
+                wait_vmcnt<0>();             // the last S - 1 stages: nothing newer to keep
+            }
+            asm volatile("" ::: "memory");   // no LDS read moves above the wait
+            compute(st);
+            asm volatile("" ::: "memory");   // ... nor the next copies above these reads
+        }
+    }
+    f32x4 fin[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) fin[t] = acc[t][0] + acc[t][1];
+
+    // Waves of the same rows meet in LDS (every ring is idle: the last stage
+    // waited for vmcnt 0) and are added in kw order; tile t of a row group is
+    // finished by the wave with kw == t % KW.
+    f32x4 *red = reinterpret_cast<f32x4 *>(lds);
+    if constexpr (KW > 1) {
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NT; ++t) red[((kw * NW + nw) * NT + t) * 64 + lane] = fin[t];
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < TILES; ++i) {
+    for (int t = 0; t < NT; ++t) {
         f32x4 s;
         if constexpr (KW > 1) {
-            if (i % KW != kw) continue;
-            s = red[0][nw][i][lane];
+            if (t % KW != kw) continue;
+            s = red[(nw * NT + t) * 64 + lane];
 #pragma unroll
-            for (int w = 1; w < KW; ++w) s += red[w][nw][i][lane];
+            for (int w = 1; w < KW; ++w) s += red[((w * NW + nw) * NT + t) * 64 + lane];
         } else {
-            s = acc[i / MT][i % MT];
+            s = fin[t];
         }
         // D of a 16x16 tile: lane l holds column m = l % 16 and rows
         // n = 4 (l / 16) + e: four consecutive outputs of row m.
-        const int t = i / MT, mt = i % MT;
-        const uint32_t m = mt * 16 + r16;
+        const uint32_t m = r16;
         const uint32_t nb = n0 + t * 16 + 4 * g;
         if (m >= M) continue;
         float o[4];
@@ -217,25 +259,31 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_mfma(const uint16_t *__re
     }
 }
 
-template <int F, int MT, int NT, int KW, int NW, int P>
+template <int F, int MA, int NT, int KW, int NW, int S>
 int launch_cfg(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N, uint32_t K,
                uint16_t *y, hipStream_t st) {
     const uint32_t rows = 16 * NT * NW;
     const uint32_t blocks = (N + rows - 1) / rows;
-    hipLaunchKernelGGL((skinny_mfma<F, MT, NT, KW, NW, P>), dim3(blocks), dim3(64 * KW * NW), 0, st, x, codes,
+    hipLaunchKernelGGL((skinny_rows<F, MA, NT, KW, NW, S>), dim3(blocks), dim3(64 * KW * NW), 0, st, x, codes,
                        scales, M, N, K, y);
-    return check_launch("skinny_mfma");
+    return check_launch("skinny_rows");
 }
 
-template <int F, int MT>
-int launch_mt(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N, uint32_t K,
+// One block per CU at these LDS sizes (96-144 KB), so the grid is sized for a
+// single round: the fewest rows per block (16, 32, 64 or 128) whose grid fits
+// on the CUs; narrow blocks split K over their waves.
+template <int F, int MA>
+int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N, uint32_t K,
               uint16_t *y, hipStream_t st) {
-    // Enough waves for the chip (about 8 per CU): 32-row blocks of 4 waves on
-    // wide matrices, 16-row blocks of 8 waves (K split 8 ways) otherwise.
-    constexpr int P = 4;   // prefetch depth in 128-code chunks
-    const uint32_t want = 8u * (uint32_t)device_props().cus;
-    if ((N + 31) / 32 * 4 >= want) return launch_cfg<F, MT, 2, 4, 1, P>(x, codes, scales, M, N, K, y, st);
-    return launch_cfg<F, MT, 1, 8, 1, P>(x, codes, scales, M, N, K, y, st);
+    const uint32_t cus = (uint32_t)device_props().cus;
+    constexpr int S3 = MA == 8 ? 3 : 2;   // ring depth of the 2-tile configurations (LDS)
+    if ((N + 15) / 16 <= cus) {
+        if constexpr (MA == 8) return launch_cfg<F, MA, 1, 8, 1, 2>(x, codes, scales, M, N, K, y, st);
+        else return launch_cfg<F, MA, 1, 4, 1, 3>(x, codes, scales, M, N, K, y, st);
+    }
+    if ((N + 31) / 32 <= cus) return launch_cfg<F, MA, 2, 4, 1, 2>(x, codes, scales, M, N, K, y, st);
+    if ((N + 63) / 64 <= cus) return launch_cfg<F, MA, 2, 2, 2, S3>(x, codes, scales, M, N, K, y, st);
+    return launch_cfg<F, MA, 2, 1, 4, S3>(x, codes, scales, M, N, K, y, st);
 }
 
 }  // namespace skinny
@@ -244,8 +292,12 @@ int launch_mt(const uint16_t *x, const uint8_t *codes, const float *scales, uint
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st) {
     using namespace skinny;
-    if (format == RENG_HIP_E4M3) return launch_mt<RENG_HIP_E4M3, 1>(x, codes, scales, M, N, K, y, st);
-    return launch_mt<RENG_HIP_E5M2, 1>(x, codes, scales, M, N, K, y, st);
+    if (M <= 8) {
+        if (format == RENG_HIP_E4M3) return launch_ma<RENG_HIP_E4M3, 8>(x, codes, scales, M, N, K, y, st);
+        return launch_ma<RENG_HIP_E5M2, 8>(x, codes, scales, M, N, K, y, st);
+    }
+    if (format == RENG_HIP_E4M3) return launch_ma<RENG_HIP_E4M3, 16>(x, codes, scales, M, N, K, y, st);
+    return launch_ma<RENG_HIP_E5M2, 16>(x, codes, scales, M, N, K, y, st);
 }
 
 }  // namespace reng
