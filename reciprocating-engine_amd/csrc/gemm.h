@@ -12,6 +12,12 @@ int launch_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales, u
 // 4 < M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st);
+// 16 < M <= 64 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
+int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
+                       uint32_t K, int format, uint16_t *y, hipStream_t st);
+// A grow-only f32 workspace of at least `floats` for split-K partials, one per
+// (device, stream) (csrc/gemm.hip); sets *rc.
+float *split_workspace(size_t floats, hipStream_t st, int *rc);
 int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, const uint8_t *b,
                     int fb, const float *sb, uint32_t nsb, uint32_t M, uint32_t N, uint32_t K,
                     uint16_t *out, hipStream_t st);

@@ -3,10 +3,8 @@
 // 1. gemv_w8a16     (M <= 4): y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]).
 //    Streams the codes once with 16-byte loads, decodes in registers
 //    (v_cvt_pk_f32_fp8 / _bf8), f32 FMA, one wave per output row.
-// 2. 4 < M <= 16: the same product on bf16 MFMA, register-streaming waves
-//    (skinny.hip).
-// 3. 16 < M <= 64: skinny_w8a16 below, bf16 MFMA with the activation tile
-//    shared by the block's waves through LDS.
+// 2. 4 < M <= 64: the same product on bf16 MFMA with the codes and the
+//    activation staged through LDS (skinny.hip); larger M in tiles of 64.
 // (The fp8 x fp8 product of gemm_fp8_scaled is in gemm_fp8.hip.)
 //
 // The reference semantics are gemm_cpu over Quantized::dequantize
@@ -188,156 +186,6 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 
 // ------------------------------------------------------------------ skinny GEMM
 
-// 4 < M <= 64 on bf16 MFMA (v_mfma_f32_16x16x32_bf16), D[n][m] = W[n][k] X[m][k]:
-// codes are the A operand (16 output rows x 32 k per MFMA, decoded to bf16 in
-// registers), the activation the B operand (16 columns m).
-//
-// Block = 4 waves on BN = 64 * AF rows; wave w owns AF fragments of 16 rows.
-// K is walked in steps of 128 codes. Each step's activation tile x[0:16MT,
-// k0:k0+128] is staged once per block in LDS (double-buffered, one barrier per
-// step) and read by every wave, so the activation crosses L2 once per 64*AF
-// rows. Within a step, lane l owns row (l % 16) of each fragment and the 32
-// consecutive codes [32 (l / 16), +32): four MFMA k-slices of 8. The B fragment
-// uses the same k assignment (a permutation of k shared by both operands).
-// The next step's codes and activation tile are loaded before the current
-// step's MFMAs. Split-K over blockIdx.y writes f32 partials to part[y][m][n]
-// (summed in a fixed order by skinny_epilogue); with one split the block
-// writes bf16 y directly.
-constexpr int SK_STEP = 128, SK_PAD = 8;
-
-template <int F, int MT, int AF>
-__global__ __launch_bounds__(256) void skinny_w8a16(const uint16_t *__restrict__ x,
-                                                    const uint8_t *__restrict__ codes,
-                                                    const float *__restrict__ scales, uint32_t M,
-                                                    uint32_t N, uint32_t K, uint32_t steps_per_split,
-                                                    uint16_t *__restrict__ y, float *__restrict__ part) {
-    constexpr int XR = 16 * MT;                 // activation rows in the tile
-    constexpr int XS = SK_STEP + SK_PAD;        // LDS row stride, bf16
-    constexpr int XV = XR * SK_STEP / 8 / 256;  // 16-byte activation vectors per thread per step
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][XR * XS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r16 = lane & 15, g4 = lane >> 4;
-    const uint32_t n0 = blockIdx.x * (64 * AF) + wave * (16 * AF);
-    const uint32_t steps = K / SK_STEP;
-    const uint32_t s0 = blockIdx.y * steps_per_split;
-    const uint32_t s1 = s0 + steps_per_split < steps ? s0 + steps_per_split : steps;
-
-    // This thread's activation vectors of a step: vector v = it * 256 + tid of
-    // the XR x 16 vectors, row v / 16, 8 bf16 at column (v % 16) * 8.
-    auto load_x = [&](uint32_t st, u32x4 (&xv)[XV]) {
-#pragma unroll
-        for (int it = 0; it < XV; ++it) {
-            const int v = it * 256 + tid, row = v >> 4, col = (v & 15) * 8;
-            xv[it] = (uint32_t)row < M ? *reinterpret_cast<const u32x4 *>(x + (size_t)row * K + st * SK_STEP + col)
-                                       : u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    auto store_x = [&](int buf, const u32x4 (&xv)[XV]) {
-#pragma unroll
-        for (int it = 0; it < XV; ++it) {
-            const int v = it * 256 + tid, row = v >> 4, col = (v & 15) * 8;
-            *reinterpret_cast<u32x4 *>(&xs[buf][row * XS + col]) = xv[it];
-        }
-    };
-    auto load_w = [&](uint32_t st, u32x4 (&q)[AF][2]) {
-#pragma unroll
-        for (int f = 0; f < AF; ++f) {
-            uint32_t n = n0 + f * 16 + r16;
-            n = n < N ? n : N - 1;   // clamped reads; stores are masked
-            const u32x4 *wp = reinterpret_cast<const u32x4 *>(codes + (size_t)n * K + st * SK_STEP + 32 * g4);
-            q[f][0] = __builtin_nontemporal_load(wp);
-            q[f][1] = __builtin_nontemporal_load(wp + 1);
-        }
-    };
-
-    f32x4 acc[AF][MT];
-#pragma unroll
-    for (int f = 0; f < AF; ++f)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    u32x4 q[AF][2], qn[AF][2], xv[XV];
-    load_w(s0, q);
-    load_x(s0, xv);
-    store_x(0, xv);
-    __syncthreads();
-    for (uint32_t st = s0; st < s1; ++st) {
-        const int buf = (st - s0) & 1;
-        const uint32_t nx = st + 1 < s1 ? st + 1 : s1 - 1;   // clamped: no branch around the loads
-        load_w(nx, qn);
-        load_x(nx, xv);
-        bf16x8 a[AF][4];
-#pragma unroll
-        for (int f = 0; f < AF; ++f) {
-            const uint32_t d[8] = {q[f][0].x, q[f][0].y, q[f][0].z, q[f][0].w,
-                                   q[f][1].x, q[f][1].y, q[f][1].z, q[f][1].w};
-#pragma unroll
-            for (int sl = 0; sl < 4; ++sl) {
-                const bf16x2 p0 = dec2_bf16<F>(d[2 * sl], false), p1 = dec2_bf16<F>(d[2 * sl], true);
-                const bf16x2 p2 = dec2_bf16<F>(d[2 * sl + 1], false), p3 = dec2_bf16<F>(d[2 * sl + 1], true);
-                a[f][sl] = bf16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const uint16_t *xr = &xs[buf][(t * 16 + r16) * XS + 32 * g4];
-#pragma unroll
-            for (int sl = 0; sl < 4; ++sl) {
-                const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(xr + 8 * sl));
-#pragma unroll
-                for (int f = 0; f < AF; ++f)
-                    acc[f][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[f][sl], b, acc[f][t], 0, 0, 0);
-            }
-        }
-        store_x(buf ^ 1, xv);   // buf ^ 1 was last read before the previous barrier
-#pragma unroll
-        for (int f = 0; f < AF; ++f) {
-            q[f][0] = qn[f][0];
-            q[f][1] = qn[f][1];
-        }
-        __syncthreads();
-    }
-    // D of a 16x16 tile: lane l holds column m = l % 16, rows n = 4 * (l / 16) + e.
-#pragma unroll
-    for (int f = 0; f < AF; ++f) {
-        const uint32_t nb = n0 + f * 16 + 4 * g4;
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const uint32_t m = t * 16 + r16;
-            if (m >= M) continue;
-            if (part) {
-                float *pp = part + ((size_t)blockIdx.y * M + m) * N;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (nb + e < N) pp[nb + e] = acc[f][t][e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t n = nb + e;
-                    if (n < N) {
-                        const float sc = scales ? scales[n] : 1.0f;
-                        y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[f][t][e] * sc);
-                    }
-                }
-            }
-        }
-    }
-}
-
-// y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the split-K partials summed in order.
-__global__ void skinny_epilogue(const float *__restrict__ part, uint32_t splits, uint32_t M, uint32_t N,
-                                const float *__restrict__ scales, uint16_t *__restrict__ y) {
-    const uint64_t total = (uint64_t)M * N;
-    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        float acc = 0.0f;
-        for (uint32_t k = 0; k < splits; ++k) acc += part[k * total + i];
-        const uint32_t n = (uint32_t)(i % N);
-        const float sc = scales ? scales[n] : 1.0f;
-        y[i] = (uint16_t)f32_to_bf16_bits(acc * sc);
-    }
-}
-
 // ------------------------------------------------------------------ launchers
 
 // Split-K partials live in a grow-only f32 buffer per (device, stream): calls on
@@ -375,46 +223,6 @@ float *split_workspace(size_t floats, hipStream_t st, int *rc) {
     }
     *rc = RENG_HIP_OK;
     return e.first;
-}
-
-struct SplitPlan {
-    uint32_t splits, steps_per_split;
-};
-
-// Split K until the grid has about `want` independent units (blocks or waves).
-SplitPlan plan_splits(uint32_t tiles, uint32_t steps, uint32_t want) {
-    uint32_t splits = (want + tiles - 1) / tiles;
-    const uint32_t max_splits = steps / 2 > 0 ? steps / 2 : 1;
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-    const uint32_t sps = (steps + splits - 1) / splits;
-    return SplitPlan{(steps + sps - 1) / sps, sps};
-}
-
-int launch_epilogue(const float *part, uint32_t splits, uint32_t M, uint32_t N, const float *scales,
-                    uint16_t *y, hipStream_t st) {
-    uint64_t blocks = ((uint64_t)M * N + 255) / 256;
-    const uint64_t cap = (uint64_t)device_props().cus * 8;
-    if (blocks > cap) blocks = cap;
-    hipLaunchKernelGGL(skinny_epilogue, dim3((unsigned)blocks), dim3(256), 0, st, part, splits, M, N, scales, y);
-    return check_launch("skinny_epilogue");
-}
-
-// One launch of the LDS-shared kernel (16 < M <= 64): 128-row blocks (64 for
-// narrow N), split-K until there are ~2 blocks per CU.
-template <int F, int MT, int AF>
-int launch_skinny_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
-                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
-    const uint32_t tiles = (N + 64 * AF - 1) / (64 * AF);
-    const SplitPlan p = plan_splits(tiles, K / SK_STEP, 2u * (uint32_t)device_props().cus);
-    int rc = RENG_HIP_OK;
-    float *part = p.splits > 1 ? split_workspace((size_t)p.splits * M * N, st, &rc) : nullptr;
-    if (rc) return rc;
-    hipLaunchKernelGGL((skinny_w8a16<F, MT, AF>), dim3(tiles, p.splits), dim3(256), 0, st, x, codes, scales, M,
-                       N, K, p.steps_per_split, y, part);
-    rc = check_launch("skinny_w8a16");
-    if (rc == RENG_HIP_OK && part) rc = launch_epilogue(part, p.splits, M, N, scales, y, st);
-    return rc;
 }
 
 template <int F>
@@ -466,25 +274,11 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
 #undef RENG_GEMV
         return check_launch("gemv_w8a16");
     }
-    // Larger M: tiles of up to 64 activation rows on the MFMA kernel.
+    // Larger M: tiles of up to 64 activation rows on the MFMA kernels.
     for (uint32_t mb = 0; mb < M; mb += 64) {
         const uint32_t mt = M - mb < 64 ? M - mb : 64;
-        int rc;
-        if (mt <= 16) {
-            rc = launch_skinny_mfma(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st);
-        } else {
-            const bool wide = N >= 1024;
-            const uint16_t *xb = x + (size_t)mb * K;
-            uint16_t *yb = y + (size_t)mb * N;
-            switch ((mt + 15) / 16) {
-                case 2: rc = wide ? launch_skinny_t<F, 2, 2>(xb, codes, scales, mt, N, K, yb, st)
-                                  : launch_skinny_t<F, 2, 1>(xb, codes, scales, mt, N, K, yb, st); break;
-                case 3: rc = wide ? launch_skinny_t<F, 3, 2>(xb, codes, scales, mt, N, K, yb, st)
-                                  : launch_skinny_t<F, 3, 1>(xb, codes, scales, mt, N, K, yb, st); break;
-                default: rc = wide ? launch_skinny_t<F, 4, 2>(xb, codes, scales, mt, N, K, yb, st)
-                                   : launch_skinny_t<F, 4, 1>(xb, codes, scales, mt, N, K, yb, st); break;
-            }
-        }
+        const int rc = mt <= 16 ? launch_skinny_mfma(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st)
+                                : launch_skinny_wide(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st);
         if (rc) return rc;
     }
     return RENG_HIP_OK;

@@ -1,5 +1,5 @@
 // skinny.hip - y[m, n] = bf16(s[n] * sum_k x[m, k] * decode(c[n, k])) for
-// 4 < M <= 16 activation rows (bf16) on bf16 MFMA (gfx950).
+// 4 < M <= 64 activation rows (bf16) on bf16 MFMA (gfx950).
 //
 // The reference semantics are gemm_cpu over Quantized::dequantize
 // (crates/reng-model/src/bin/fp8_probe.rs:55-67) with the per-channel scaleB
@@ -10,7 +10,9 @@
 // instruction: that pattern streams HBM at ~4 TB/s on this device against
 // ~5.5 TB/s for 4 rows x 256 bytes. So the codes (and the activation) go
 // through LDS: copied in 4 x 256-byte pieces by global_load_lds and read back
-// transposed (skinny_rows below). One launch, no partial sums in memory.
+// transposed (skinny_rows for M <= 16: one launch, no partial sums in memory;
+// skinny_wide for 16 < M <= 64, where a block must cover many weight rows per
+// activation byte it reads and so splits K over blocks).
 #include <type_traits>
 
 #include "common.h"
@@ -64,6 +66,18 @@ __device__ __forceinline__ void wait_vmcnt() {
 // instantiation.
 __device__ __forceinline__ void copy16(const uint8_t *g, uint8_t *l) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
+}
+
+// s_waitcnt lgkmcnt(0): this wave's LDS reads have returned, so copies may
+// overwrite the slot they read.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+// A workgroup barrier without the vmcnt(0) of __syncthreads' fence; the memory
+// clobbers keep LDS accesses on their side of it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // A block of KW x NW waves owns 16 NT NW weight rows; wave (kw, nw) takes the
@@ -200,6 +214,7 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
             if ((uint32_t)s < nst) copies(s);
         for (uint32_t st = 0; st < nst; ++st) {
             if (st + S - 1 < nst) {
+                wait_lgkm0();                // slot (st - 1) % S has been read
                 copies(st + S - 1);
                 wait_vmcnt<(S - 1) * C>();   // stage st has landed; S - 1 newer stages in flight
             } else {
@@ -286,6 +301,240 @@ int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint
     return launch_cfg<F, MA, 2, 1, 4, S3>(x, codes, scales, M, N, K, y, st);
 }
 
+
+// 16 < M <= 64. The activation is 128 bytes per k at M = 64 against R bytes
+// of codes for R weight rows, so a block covers R = 32 NTW rows (64 or 128)
+// and shares one copy of each stage between its 4 waves: stages of BK = 128
+// codes in an S-slot LDS ring (one barrier per stage), filled by global_load_lds
+//   codes: R / 8 copies of 8 rows x 128 bytes, piece p of row r in slot p ^ swz8(r);
+//   activation: 16 MT rows (>= M repeat row M - 1), 4 rows x 256 bytes per copy,
+//     8-element piece p of row r in slot p ^ (r % 16);
+// spread over the waves. Wave (wn, wm) computes rows [wn R / 2, +R / 2) against
+// activation tiles wm, wm + 2 (< MT). Blocks split K (blockIdx.y takes chunks
+// [y cps, +cps)) until the grid fills the CUs; with more than one split the
+// partial products go to part[y][m][n] (f32, 16-byte stores) and
+// reduce_splits adds them in split order.
+__device__ __forceinline__ uint32_t swz8(uint32_t r) { return (r ^ ((r >> 3) & 1)) & 7; }
+
+template <int F, int MT, int NTW, int S>
+__global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes,
+                                                   const float *__restrict__ scales, uint32_t M, uint32_t N,
+                                                   uint32_t K, uint32_t cps, uint16_t *__restrict__ y,
+                                                   float *__restrict__ part) {
+    constexpr int BK = CHUNK, R = 32 * NTW, AR = 16 * MT;
+    constexpr int WB = R * BK, AB = AR * BK * 2, SLOT = WB + AB;
+    constexpr int WC = R / 8, AC = AR / 4;          // copies per stage (block)
+    static_assert(WC % 4 == 0 && AC % 4 == 0, "copies split evenly over 4 waves");
+    constexpr int C = (WC + AC) / 4;                // copies per stage per wave
+    static_assert(S >= 2 && (S - 2) * C < 64, "vmcnt");
+    constexpr int MTW = (MT + 1) / 2;               // activation tiles per wave
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * SLOT];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave >> 1, wm = wave & 1;
+    const uint32_t r16 = lane & 15, g = lane >> 4;
+    const uint32_t n0 = blockIdx.x * R;
+    const uint32_t chunks = K / CHUNK;
+    const uint32_t kc0 = blockIdx.y * cps, kc1 = kc0 + cps < chunks ? kc0 + cps : chunks;
+    const uint32_t nst = kc1 - kc0;
+
+    // This wave's copies q = wave + 4 c: q < WC a code copy, else activation copy q - WC.
+    const uint8_t *src[C];
+    uint32_t dst[C], unit[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int q = wave + 4 * c;
+        if (q < WC) {
+            const uint32_t rr = q * 8 + lane / 8, p = (lane % 8) ^ swz8(rr);
+            uint32_t n = n0 + rr;
+            n = n < N ? n : N - 1;   // rows past N are read but never stored
+            src[c] = codes + (size_t)n * K + (size_t)kc0 * CHUNK + p * 16;
+            dst[c] = q * 1024;
+            unit[c] = 1;
+        } else {
+            const int qa = q - WC;
+            const uint32_t row = qa * 4 + lane / 16, p = (lane % 16) ^ (row & 15);
+            const uint32_t m = row < M ? row : M - 1;
+            src[c] = reinterpret_cast<const uint8_t *>(x + (size_t)m * K + (size_t)kc0 * CHUNK + p * 8);
+            dst[c] = WB + qa * 1024;
+            unit[c] = 2;
+        }
+    }
+    auto copies = [&](uint32_t st) {
+        uint8_t *slot = lds + (st % S) * SLOT;
+#pragma unroll
+        for (int c = 0; c < C; ++c) copy16(src[c] + (size_t)st * BK * unit[c], slot + dst[c]);
+    };
+
+    f32x4 acc[NTW][MTW];
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+#pragma unroll
+        for (int u = 0; u < MTW; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](uint32_t st) {
+        const uint8_t *slot = lds + (st % S) * SLOT;
+        u32x4 w[NTW][2];
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) {
+            const uint32_t rr = wn * (R / 2) + t * 16 + r16;
+            const uint8_t *rb = slot + rr * BK;
+            w[t][0] = *reinterpret_cast<const u32x4 *>(rb + ((g ^ swz8(rr)) * 16));
+            w[t][1] = *reinterpret_cast<const u32x4 *>(rb + (((4 + g) ^ swz8(rr)) * 16));
+        }
+        u32x4 a[MTW][4];
+#pragma unroll
+        for (int u = 0; u < MTW; ++u) {
+            const int mt = wm + 2 * u;
+            uint32_t am = (mt < MT ? mt : MT - 1) * 16 + r16;
+            am = am < M ? am : M - 1;
+            const uint8_t *arow = slot + WB + am * (BK * 2);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t p = 2 * g + (j & 1) + 8 * (j >> 1);
+                a[u][j] = *reinterpret_cast<const u32x4 *>(arow + ((p ^ (am & 15)) * 16));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int t = 0; t < NTW; ++t) {
+                const u32x4 &q = w[t][j >> 1];
+                const bf16x8 wa = (j & 1) ? dec8<F>(q.z, q.w) : dec8<F>(q.x, q.y);
+#pragma unroll
+                for (int u = 0; u < MTW; ++u) {
+                    if (wm + 2 * u >= MT) break;
+                    acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, __builtin_bit_cast(bf16x8, a[u][j]),
+                                                                       acc[t][u], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if ((uint32_t)s < nst) copies(s);
+    for (uint32_t st = 0; st < nst; ++st) {
+        if (st + S - 2 < nst) wait_vmcnt<(S - 2) * C>();   // own copies of stage st landed
+        else wait_vmcnt<0>();
+        wait_lgkm0();
+        lds_barrier();   // everyone's copies of st landed; slot (st - 1) % S has been read
+        if (st + S - 1 < nst) copies(st + S - 1);
+        compute(st);
+    }
+
+    // Lane holds column m = 16 mt + l % 16 and rows n = 4 (l / 16) + e.
+#pragma unroll
+    for (int u = 0; u < MTW; ++u) {
+        const int mt = wm + 2 * u;
+        if (mt >= MT) break;
+        const uint32_t m = mt * 16 + r16;
+        if (m >= M) continue;
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) {
+            const uint32_t nb = n0 + wn * (R / 2) + t * 16 + 4 * g;
+            const f32x4 s = acc[t][u];
+            if (part) {
+                float *pp = part + ((size_t)blockIdx.y * M + m) * N;
+                if (nb + 3 < N && (N & 3) == 0) {
+                    *reinterpret_cast<f32x4 *>(pp + nb) = s;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (nb + e < N) pp[nb + e] = s[e];
+                }
+            } else {
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t n = nb + e < N ? nb + e : N - 1;
+                    o[e] = s[e] * (scales ? scales[n] : 1.0f);
+                }
+                uint16_t *yr = y + (size_t)m * N;
+                if (nb + 3 < N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+                    *reinterpret_cast<u32x2 *>(yr + nb) =
+                        u32x2{f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16),
+                              f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16)};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (nb + e < N) yr[nb + e] = (uint16_t)f32_to_bf16_bits(o[e]);
+                }
+            }
+        }
+    }
+}
+
+// y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the splits added in order; four
+// consecutive n per thread when N % 4 == 0 (16-byte reads, 8-byte stores).
+__global__ void reduce_splits(const float *__restrict__ part, uint32_t splits, uint32_t M, uint32_t N,
+                              const float *__restrict__ scales, uint16_t *__restrict__ y) {
+    const uint64_t total = (uint64_t)M * N;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+        for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total / 4; i += step) {
+            f32x4 a = reinterpret_cast<const f32x4 *>(part)[i];
+            for (uint32_t k = 1; k < splits; ++k) a += reinterpret_cast<const f32x4 *>(part + k * total)[i];
+            const uint32_t n = (uint32_t)((4 * i) % N);
+            const f32x4 sc = scales ? *reinterpret_cast<const f32x4 *>(scales + n) : f32x4{1.f, 1.f, 1.f, 1.f};
+            reinterpret_cast<u32x2 *>(y)[i] =
+                u32x2{f32_to_bf16_bits(a.x * sc.x) | (f32_to_bf16_bits(a.y * sc.y) << 16),
+                      f32_to_bf16_bits(a.z * sc.z) | (f32_to_bf16_bits(a.w * sc.w) << 16)};
+        }
+    } else {
+        for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total; i += step) {
+            float a = part[i];
+            for (uint32_t k = 1; k < splits; ++k) a += part[k * total + i];
+            y[i] = (uint16_t)f32_to_bf16_bits(a * (scales ? scales[i % N] : 1.0f));
+        }
+    }
+}
+
+// Grid: ceil(N / R) row tiles times K splits, about one block per CU (the
+// ring takes 128-144 KB of LDS).
+template <int F, int MT, int NTW, int S>
+int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
+                    uint32_t K, uint16_t *y, hipStream_t st) {
+    const uint32_t tiles = (N + 32 * NTW - 1) / (32 * NTW);
+    const uint32_t chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
+    uint32_t splits = cus / tiles;
+    splits = splits < 1 ? 1 : splits > chunks ? chunks : splits;
+    const uint32_t cps = (chunks + splits - 1) / splits;
+    splits = (chunks + cps - 1) / cps;
+    int rc = RENG_HIP_OK;
+    float *part = splits > 1 ? split_workspace((size_t)splits * M * N, st, &rc) : nullptr;
+    if (rc) return rc;
+    hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S>), dim3(tiles, splits), dim3(256), 0, st, x, codes, scales, M, N,
+                       K, cps, y, part);
+    rc = check_launch("skinny_wide");
+    if (rc || !part) return rc;
+    uint64_t blocks = ((uint64_t)M * N / 4 + 255) / 256;
+    blocks = blocks < 1 ? 1 : blocks > 4ull * cus ? 4ull * cus : blocks;
+    hipLaunchKernelGGL(reduce_splits, dim3((unsigned)blocks), dim3(256), 0, st, part, splits, M, N, scales, y);
+    return check_launch("reduce_splits");
+}
+
+template <int F, int MT>
+int launch_wide_mt(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
+                   uint32_t K, uint16_t *y, hipStream_t st) {
+    // 64-row blocks for small matrices (fewer splits: the partials cost more
+    // than the activation re-reads there), else 128 (half the activation
+    // bytes per code).
+    if ((uint64_t)N * K <= (16ull << 20)) return launch_wide_cfg<F, MT, 2, 6>(x, codes, scales, M, N, K, y, st);
+    return launch_wide_cfg<F, MT, 4, 4>(x, codes, scales, M, N, K, y, st);
+}
+
+template <int F>
+int launch_wide_f(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
+                  uint32_t K, uint16_t *y, hipStream_t st) {
+    switch ((M + 15) / 16) {
+        case 2: return launch_wide_mt<F, 2>(x, codes, scales, M, N, K, y, st);
+        case 3: return launch_wide_mt<F, 3>(x, codes, scales, M, N, K, y, st);
+        default: return launch_wide_mt<F, 4>(x, codes, scales, M, N, K, y, st);
+    }
+}
+
 }  // namespace skinny
 
 // 4 < M <= 16, K % 128 == 0.
@@ -298,6 +547,14 @@ int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *sca
     }
     if (format == RENG_HIP_E4M3) return launch_ma<RENG_HIP_E4M3, 16>(x, codes, scales, M, N, K, y, st);
     return launch_ma<RENG_HIP_E5M2, 16>(x, codes, scales, M, N, K, y, st);
+}
+
+// 16 < M <= 64, K % 128 == 0.
+int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
+                       uint32_t K, int format, uint16_t *y, hipStream_t st) {
+    using namespace skinny;
+    if (format == RENG_HIP_E4M3) return launch_wide_f<RENG_HIP_E4M3>(x, codes, scales, M, N, K, y, st);
+    return launch_wide_f<RENG_HIP_E5M2>(x, codes, scales, M, N, K, y, st);
 }
 
 }  // namespace reng
