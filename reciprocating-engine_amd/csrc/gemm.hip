@@ -110,10 +110,23 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
         }
     };
 
-    // The first group's codes are requested before the activation is staged.
+    // The first group's codes and the scales are requested before the
+    // activation is staged.
     uint32_t r = wave, gi = 0;
     u32x4 qn[CPL];
-    if (wave < N) load(r, gi, qn);
+    // Lane j holds the scale of this wave's row ri + j (ri = rows done,
+    // refilled every 64 rows), so an end-of-row multiply reads it with
+    // readlane instead of waiting a memory round trip.
+    uint32_t ri = 0;
+    float sv = 1.0f;
+    auto scales_from = [&](uint32_t first) {   // lanes past the last row repeat it (never read)
+        const uint32_t rr = wave + (first + lane) * waves;
+        sv = scales[rr < N ? rr : N - 1];
+    };
+    if (wave < N) {
+        load(r, gi, qn);
+        if (scales) scales_from(0);
+    }
     if constexpr (XLDS) {
         const u32x4 *src = reinterpret_cast<const u32x4 *>(x);
         u32x4 *dst = reinterpret_cast<u32x4 *>(xs);
@@ -170,7 +183,8 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
             }
         }
         if (gi + 1 == gpr) {   // end of row r: reduce across the wave and store
-            const float s = scales ? scales[r] : 1.0f;
+            const float s = scales ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), ri & 63)) : 1.0f;
+            if (scales && (++ri & 63) == 0) scales_from(ri);
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 const float t = wave_sum_dpp(acc[m][0] + acc[m][1]);

@@ -106,6 +106,14 @@ def test_gemv_small_batches(R, M):
     check_w8a16(R, rng, M, 100, 176, E5M2)
 
 
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv_many_rows_per_wave(R, M):
+    """N = 300000 short rows: ~74 rows per wave, past the 64 per-row scales a
+    wave holds at a time (the refill path), with a ragged chunk count."""
+    rng = np.random.default_rng(211 + M)
+    check_w8a16(R, rng, M, 300000, 48, E4M3, sample_cols=4096)
+
+
 QWEN_7B = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]
 
 
