@@ -147,7 +147,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
             gn = 0;
             rn = r + waves;
         }
-        load(rn, gn, qn);
+        if (rn < N) load(rn, gn, qn);   // none past the wave's last row
 
         const uint32_t c0 = gi * 64 * CPL + lane;
 #pragma unroll
