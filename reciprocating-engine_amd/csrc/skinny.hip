@@ -208,6 +208,17 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
         }
     };
 
+    // The scales of this lane's output rows, requested before any copy (older
+    // than everything the explicit waits count; used after the loop).
+    float sc[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t n = n0 + t * 16 + 4 * g + e;
+            sc[t][e] = scales ? scales[n < N ? n : N - 1] : 1.0f;
+        }
+
     if (c0 < c1) {
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
@@ -257,10 +268,7 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
         if (m >= M) continue;
         float o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t n = nb + e < N ? nb + e : N - 1;
-            o[e] = s[e] * (scales ? scales[n] : 1.0f);
-        }
+        for (int e = 0; e < 4; ++e) o[e] = s[e] * sc[t][e];
         uint16_t *yr = y + (size_t)m * N;
         if (nb + 3 < N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
             *reinterpret_cast<u32x2 *>(yr + nb) =
@@ -412,6 +420,17 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
         }
     };
 
+    // Without K splits this block applies the scales: requested before any
+    // copy (older than everything the explicit waits count).
+    float sc[NTW][4];
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t n = n0 + wn * (R / 2) + t * 16 + 4 * g + e;
+            sc[t][e] = (scales && !part) ? scales[n < N ? n : N - 1] : 1.0f;
+        }
+
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
         if ((uint32_t)s < nst) copies(s);
@@ -447,10 +466,7 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
             } else {
                 float o[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t n = nb + e < N ? nb + e : N - 1;
-                    o[e] = s[e] * (scales ? scales[n] : 1.0f);
-                }
+                for (int e = 0; e < 4; ++e) o[e] = s[e] * sc[t][e];
                 uint16_t *yr = y + (size_t)m * N;
                 if (nb + 3 < N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
                     *reinterpret_cast<u32x2 *>(yr + nb) =
