@@ -484,14 +484,31 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
 
 // y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the splits added in order; four
 // consecutive n per thread when N % 4 == 0 (16-byte reads, 8-byte stores).
-__global__ void reduce_splits(const float *__restrict__ part, uint32_t splits, uint32_t M, uint32_t N,
-                              const float *__restrict__ scales, uint16_t *__restrict__ y) {
+// The split loads are issued eight at a time (independent) and added in order.
+__device__ __forceinline__ f32x4 sum_splits4(const float *part, uint32_t splits, uint64_t total, uint64_t i) {
+    const f32x4 *p = reinterpret_cast<const f32x4 *>(part) + i;
+    const uint64_t stride = total / 4;
+    f32x4 a = p[0];
+    uint32_t k = 1;
+    for (; k + 8 <= splits; k += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(k + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a += v[u];
+    }
+    for (; k < splits; ++k) a += p[k * stride];
+    return a;
+}
+
+__global__ __launch_bounds__(64) void reduce_splits(const float *__restrict__ part, uint32_t splits, uint32_t M,
+                                                    uint32_t N, const float *__restrict__ scales,
+                                                    uint16_t *__restrict__ y) {
     const uint64_t total = (uint64_t)M * N;
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
     if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
         for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total / 4; i += step) {
-            f32x4 a = reinterpret_cast<const f32x4 *>(part)[i];
-            for (uint32_t k = 1; k < splits; ++k) a += reinterpret_cast<const f32x4 *>(part + k * total)[i];
+            const f32x4 a = sum_splits4(part, splits, total, i);
             const uint32_t n = (uint32_t)((4 * i) % N);
             const f32x4 sc = scales ? *reinterpret_cast<const f32x4 *>(scales + n) : f32x4{1.f, 1.f, 1.f, 1.f};
             reinterpret_cast<u32x2 *>(y)[i] =
@@ -514,8 +531,11 @@ int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales
                     uint32_t K, uint16_t *y, hipStream_t st) {
     const uint32_t tiles = (N + 32 * NTW - 1) / (32 * NTW);
     const uint32_t chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
+    // At least 4 chunks (512 codes) per split: below that the partials
+    // outweigh the codes.
+    const uint32_t max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
     uint32_t splits = cus / tiles;
-    splits = splits < 1 ? 1 : splits > chunks ? chunks : splits;
+    splits = splits < 1 ? 1 : splits > max_splits ? max_splits : splits;
     const uint32_t cps = (chunks + splits - 1) / splits;
     splits = (chunks + cps - 1) / cps;
     int rc = RENG_HIP_OK;
@@ -525,9 +545,9 @@ int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales
                        K, cps, y, part);
     rc = check_launch("skinny_wide");
     if (rc || !part) return rc;
-    uint64_t blocks = ((uint64_t)M * N / 4 + 255) / 256;
-    blocks = blocks < 1 ? 1 : blocks > 4ull * cus ? 4ull * cus : blocks;
-    hipLaunchKernelGGL(reduce_splits, dim3((unsigned)blocks), dim3(256), 0, st, part, splits, M, N, scales, y);
+    uint64_t blocks = ((uint64_t)M * N / 4 + 63) / 64;
+    blocks = blocks < 1 ? 1 : blocks > 16ull * cus ? 16ull * cus : blocks;
+    hipLaunchKernelGGL(reduce_splits, dim3((unsigned)blocks), dim3(64), 0, st, part, splits, M, N, scales, y);
     return check_launch("reduce_splits");
 }
 
