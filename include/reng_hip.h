@@ -164,6 +164,50 @@ RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const 
                                           size_t N, size_t K, uint16_t *out, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * Decode step of one Llama decoder layer around its fp8 GEMVs
+ *
+ * The reference's fp8 load path stops at a refusal where the quantized codes
+ * would meet a device layer (layer_views, crates/reng-model/src/lib.rs:2636-2649);
+ * these entry points are the non-GEMM steps of that layer, one token per call,
+ * with the semantics of its CPU decoder layer (layer_cpu, causal, Llama form:
+ * crates/reng-synapse/src/model.rs:2903-3100). The seven projections are
+ * reng_hip_gemm_w8a16 with M = 1 on the layer's codes and scales. Residual
+ * stream f32; GEMV inputs bf16; caches bf16 [positions, n_kv_heads * head_dim].
+ * ------------------------------------------------------------------------- */
+
+/* Longest cache one reng_hip_attention_decode call reads (its scores sit in LDS). */
+#define RENG_HIP_ATTENTION_MAX_LEN 15000
+
+/* out[r, :] = bf16(x[r, :] / sqrt(mean(x[r, :]^2) + eps) * gamma), x f32
+ * [rows, cols] (rms_norm_cpu, crates/reng-synapse/src/ops.rs:49-72). */
+RENG_HIP_API int reng_hip_rms_norm_bf16(const float *x, const float *gamma, size_t rows, size_t cols, float eps,
+                                        uint16_t *out, void *stream);
+
+/* Rotate-half RoPE of one position (rope_cpu, ops.rs:118-135) with the row
+ * sin_row / cos_row [head_dim] of the tables: q [n_heads * head_dim] bf16 in
+ * place; k [n_kv_heads * head_dim] rotated into k_row and v copied into v_row
+ * (this position's rows of the key and value caches). head_dim even. */
+RENG_HIP_API int reng_hip_rope_append(uint16_t *q, const uint16_t *k, const uint16_t *v, size_t n_heads,
+                                      size_t n_kv_heads, size_t head_dim, const float *sin_row, const float *cos_row,
+                                      uint16_t *k_row, uint16_t *v_row, void *stream);
+
+/* One query per head over cache rows 0 .. len - 1 (layer_cpu's causal attention,
+ * model.rs:3010-3050): out[h] = softmax(scale * q[h] . K[:, g]) V[:, g] with
+ * g = h / (n_heads / n_kv_heads), bf16 in and out, f32 inside; 1 <= len <=
+ * RENG_HIP_ATTENTION_MAX_LEN. */
+RENG_HIP_API int reng_hip_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                                           size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t len,
+                                           float scale, uint16_t *out, void *stream);
+
+/* out = bf16(silu(gate) * up), silu(g) = g / (1 + exp(-g)) (layer_cpu's
+ * Activation::Silu, model.rs:3070-3080). */
+RENG_HIP_API int reng_hip_silu_mul_bf16(const uint16_t *gate, const uint16_t *up, size_t n, uint16_t *out,
+                                        void *stream);
+
+/* out = x + d, x f32, d bf16 (a branch output added to the residual stream). */
+RENG_HIP_API int reng_hip_add_bf16_f32(const float *x, const uint16_t *d, size_t n, float *out, void *stream);
+
+/* ---------------------------------------------------------------------------
  * Self-check (no counterpart in the reference)
  * ------------------------------------------------------------------------- */
 

@@ -1,0 +1,179 @@
+// fp8_decoder.cpp - see fp8_decoder.hpp.
+#include "fp8_decoder.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <string>
+
+#include "../../include/reng_hip.h"
+
+namespace reng_model {
+
+namespace {
+
+void hip_ok(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw Error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void abi_ok(int rc) {
+    if (rc != RENG_HIP_OK) throw Error(std::string("reng-hip: ") + reng_hip_last_error());
+}
+
+int abi_format(reng_fp8::Fp8Format f) { return f == reng_fp8::Fp8Format::E4M3 ? RENG_HIP_E4M3 : RENG_HIP_E5M2; }
+
+}  // namespace
+
+Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max_positions) {
+    if (!w.fp8) throw Error("Fp8Decoder: the weights carry no fp8 codes (load them with the fp8 switch on)");
+    if (!(cfg.model_type == "llama" || cfg.model_type == "mistral" || cfg.model_type.empty()))
+        throw Error("Fp8Decoder: model_type " + cfg.model_type +
+                    " is not implemented by the fp8 decode step (Llama form only)");
+    if (cfg.has_rope_scaling) throw Error("Fp8Decoder: rope_scaling is not implemented by the fp8 decode step");
+    if (cfg.sliding_window) throw Error("Fp8Decoder: sliding_window is not implemented by the fp8 decode step");
+    if (cfg.attention_multiplier || cfg.query_pre_attn_scalar)
+        throw Error("Fp8Decoder: an attention scale override is not implemented by the fp8 decode step");
+    hidden_ = cfg.hidden_size;
+    inter_ = cfg.intermediate_size;
+    nh_ = cfg.num_attention_heads;
+    nkv_ = cfg.n_kv_heads();
+    hd_ = cfg.head_dim();
+    eps_ = cfg.rms_norm_eps;
+    // layer_cpu's score scale for a model without overrides (lib.rs:701-705).
+    scale_ = 1.0f / std::sqrt((float)hd_);
+    max_pos_ = max_positions;
+    if (hd_ % 2 != 0 || hd_ == 0) throw Error("Fp8Decoder: head_dim " + std::to_string(hd_) + " is not even");
+    if (nkv_ == 0 || nh_ % nkv_ != 0) throw Error("Fp8Decoder: heads are not a multiple of key/value heads");
+    if (max_pos_ < 1 || max_pos_ > RENG_HIP_ATTENTION_MAX_LEN)
+        throw Error("Fp8Decoder: max_positions " + std::to_string(max_pos_) + " is not in [1, " +
+                    std::to_string(RENG_HIP_ATTENTION_MAX_LEN) + "]");
+    if (w.fp8->size() != w.layers.size()) throw Error("Fp8Decoder: fp8 layers do not match the weights");
+
+    auto dev = [&](size_t bytes) {
+        void *p = nullptr;
+        hip_ok(hipMalloc(&p, bytes > 0 ? bytes : 1), "hipMalloc");
+        allocs_.push_back(p);
+        return p;
+    };
+    auto upload = [&](const void *src, size_t bytes) {
+        void *p = dev(bytes);
+        hip_ok(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+        return p;
+    };
+    try {
+        const size_t qd = nh_ * hd_, kvd = nkv_ * hd_;
+        auto mat = [&](const reng_fp8::Quantized &q, size_t rows, size_t cols, const char *name) {
+            if (q.rows != rows || q.cols != cols)
+                throw Error(std::string("Fp8Decoder: ") + name + " is " + std::to_string(q.rows) + " x " +
+                            std::to_string(q.cols) + ", the config implies " + std::to_string(rows) + " x " +
+                            std::to_string(cols));
+            if (cols % 16 != 0) throw Error(std::string("Fp8Decoder: ") + name + " width is not a multiple of 16");
+            Mat m;
+            m.codes = static_cast<uint8_t *>(upload(q.codes.data(), q.codes.size()));
+            m.scales = static_cast<float *>(upload(q.scales.data(), q.scales.size() * sizeof(float)));
+            m.rows = rows;
+            m.cols = cols;
+            m.format = abi_format(q.format);
+            return m;
+        };
+        for (size_t li = 0; li < w.layers.size(); ++li) {
+            const LayerFp8 &f = (*w.fp8)[li];
+            const LayerTensors &t = w.layers[li];
+            Layer L;
+            L.wq = mat(f.wq, qd, hidden_, "wq");
+            L.wk = mat(f.wk, kvd, hidden_, "wk");
+            L.wv = mat(f.wv, kvd, hidden_, "wv");
+            L.wo = mat(f.wo, hidden_, qd, "wo");
+            L.wg = mat(f.wg, inter_, hidden_, "wg");
+            L.wu = mat(f.wu, inter_, hidden_, "wu");
+            L.wd = mat(f.wd, hidden_, inter_, "wd");
+            if (t.g1.size() != hidden_ || t.g2.size() != hidden_) throw Error("Fp8Decoder: norm gains are not [hidden]");
+            L.g1 = static_cast<float *>(upload(t.g1.data(), hidden_ * sizeof(float)));
+            L.g2 = static_cast<float *>(upload(t.g2.data(), hidden_ * sizeof(float)));
+            L.kcache = static_cast<uint16_t *>(dev(max_pos_ * kvd * 2));
+            L.vcache = static_cast<uint16_t *>(dev(max_pos_ * kvd * 2));
+            layers_.push_back(L);
+        }
+        // rope_caches (lib.rs:1970-1972, 2188-2215 with rotary_dim = head_dim):
+        // entry (p, d) = sin / cos(p * theta^(-2 (d % half) / head_dim)).
+        std::vector<float> sn(max_pos_ * hd_), cs(max_pos_ * hd_);
+        const size_t half = hd_ / 2;
+        for (size_t p = 0; p < max_pos_; ++p)
+            for (size_t d = 0; d < hd_; ++d) {
+                const float inv = std::pow(cfg.rope_theta, -2.0f * (float)(d % half) / (float)hd_);
+                const float ang = (float)p * inv;
+                sn[p * hd_ + d] = std::sin(ang);
+                cs[p * hd_ + d] = std::cos(ang);
+            }
+        sin_ = static_cast<float *>(upload(sn.data(), sn.size() * sizeof(float)));
+        cos_ = static_cast<float *>(upload(cs.data(), cs.size() * sizeof(float)));
+        x_ = static_cast<float *>(dev(hidden_ * 4));
+        h_ = static_cast<float *>(dev(hidden_ * 4));
+        // bf16 buffers 16-byte aligned (hipMalloc) for the GEMV's inputs.
+        n_ = static_cast<uint16_t *>(dev(hidden_ * 2));
+        q_ = static_cast<uint16_t *>(dev(qd * 2));
+        k_ = static_cast<uint16_t *>(dev(kvd * 2));
+        v_ = static_cast<uint16_t *>(dev(kvd * 2));
+        a_ = static_cast<uint16_t *>(dev(qd * 2));
+        o_ = static_cast<uint16_t *>(dev(hidden_ * 2));
+        gate_ = static_cast<uint16_t *>(dev(inter_ * 2));
+        up_ = static_cast<uint16_t *>(dev(inter_ * 2));
+        act_ = static_cast<uint16_t *>(dev(inter_ * 2));
+        down_ = static_cast<uint16_t *>(dev(hidden_ * 2));
+    } catch (...) {
+        for (void *p : allocs_) (void)hipFree(p);
+        allocs_.clear();
+        throw;
+    }
+}
+
+Fp8Decoder::~Fp8Decoder() {
+    (void)hipDeviceSynchronize();
+    for (void *p : allocs_) (void)hipFree(p);
+}
+
+void Fp8Decoder::gemv(const Mat &m, const uint16_t *x, uint16_t *y, void *stream) {
+    abi_ok(reng_hip_gemm_w8a16(x, m.codes, m.scales, 1, m.rows, m.cols, m.format, y, stream));
+}
+
+void Fp8Decoder::step_device(size_t li, const float *x, float *y, size_t pos, void *stream) {
+    Layer &L = layers_.at(li);
+    if (pos != L.pos)
+        throw Error("Fp8Decoder: layer " + std::to_string(li) + " is at position " + std::to_string(L.pos) +
+                    ", asked for " + std::to_string(pos));
+    if (pos >= max_pos_) throw Error("Fp8Decoder: position " + std::to_string(pos) + " is past the cache");
+    const size_t kvd = nkv_ * hd_;
+    abi_ok(reng_hip_rms_norm_bf16(x, L.g1, 1, hidden_, eps_, n_, stream));
+    gemv(L.wq, n_, q_, stream);
+    gemv(L.wk, n_, k_, stream);
+    gemv(L.wv, n_, v_, stream);
+    abi_ok(reng_hip_rope_append(q_, k_, v_, nh_, nkv_, hd_, sin_ + pos * hd_, cos_ + pos * hd_,
+                                L.kcache + pos * kvd, L.vcache + pos * kvd, stream));
+    abi_ok(reng_hip_attention_decode(q_, L.kcache, L.vcache, nh_, nkv_, hd_, pos + 1, scale_, a_, stream));
+    gemv(L.wo, a_, o_, stream);
+    abi_ok(reng_hip_add_bf16_f32(x, o_, hidden_, h_, stream));
+    abi_ok(reng_hip_rms_norm_bf16(h_, L.g2, 1, hidden_, eps_, n_, stream));
+    gemv(L.wg, n_, gate_, stream);
+    gemv(L.wu, n_, up_, stream);
+    abi_ok(reng_hip_silu_mul_bf16(gate_, up_, inter_, act_, stream));
+    gemv(L.wd, act_, down_, stream);
+    abi_ok(reng_hip_add_bf16_f32(h_, down_, hidden_, y, stream));
+    ++L.pos;
+}
+
+std::vector<float> Fp8Decoder::step(size_t li, const std::vector<float> &x, size_t pos) {
+    if (x.size() != hidden_)
+        throw Error("Fp8Decoder: input row has " + std::to_string(x.size()) + " values, hidden is " +
+                    std::to_string(hidden_));
+    hip_ok(hipMemcpy(x_, x.data(), hidden_ * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    step_device(li, x_, x_, pos, nullptr);
+    std::vector<float> y(hidden_);
+    hip_ok(hipMemcpy(y.data(), x_, hidden_ * 4, hipMemcpyDeviceToHost), "hipMemcpy");
+    return y;
+}
+
+void Fp8Decoder::reset() {
+    for (Layer &L : layers_) L.pos = 0;
+}
+
+}  // namespace reng_model

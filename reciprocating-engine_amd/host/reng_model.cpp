@@ -157,6 +157,11 @@ LlamaConfig LlamaConfig::from_json(const std::string &text) {
         if (auto *p = opt("num_key_value_heads")) c.num_key_value_heads = p->as_u64();
         if (auto *p = opt("head_dim")) c.head_dim_ = p->as_u64();
         if (auto *p = opt("tie_word_embeddings")) c.tie_word_embeddings = p->b;
+        if (auto *p = opt("rope_theta")) c.rope_theta = (float)p->as_f64();
+        c.has_rope_scaling = opt("rope_scaling") != nullptr;
+        if (auto *p = opt("sliding_window")) c.sliding_window = p->as_u64();
+        if (auto *p = opt("attention_multiplier")) c.attention_multiplier = (float)p->as_f64();
+        if (auto *p = opt("query_pre_attn_scalar")) c.query_pre_attn_scalar = (float)p->as_f64();
     } catch (const Error &) {
         throw;
     } catch (const std::exception &e) {

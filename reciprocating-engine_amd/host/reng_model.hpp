@@ -35,6 +35,14 @@ struct LlamaConfig {
     // Where the language model's tensors live: "model." (default) or
     // "language_model.model." for a multimodal config.
     std::string weight_prefix = "model.";
+    // RoPE and attention settings the decode step reads (lib.rs:100-200):
+    // rope_theta (1e4 when absent); the presence of rope_scaling, of a
+    // sliding window and of the scale overrides, which the fp8 decode step
+    // does not implement and refuses.
+    float rope_theta = 10000.0f;
+    bool has_rope_scaling = false;
+    std::optional<size_t> sliding_window;
+    std::optional<float> attention_multiplier, query_pre_attn_scalar;
 
     size_t n_kv_heads() const { return num_key_value_heads.value_or(num_attention_heads); }
     size_t head_dim() const { return head_dim_.value_or(hidden_size / num_attention_heads); }

@@ -59,6 +59,11 @@ SIGNATURES = {
     "reng_hip_gemm_w8a16": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _I, _P, _P]),
     "reng_hip_gemm_fp8_scaled": (_I, [_P, _I, _P, _SZ, _P, _I, _P, _SZ, _SZ, _SZ, _SZ, _P, _P]),
     "reng_hip_verify_hw_convert": (_I, [_I, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32)]),
+    "reng_hip_rms_norm_bf16": (_I, [_P, _P, _SZ, _SZ, _F, _P, _P]),
+    "reng_hip_rope_append": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P]),
+    "reng_hip_attention_decode": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _P]),
+    "reng_hip_silu_mul_bf16": (_I, [_P, _P, _SZ, _P, _P]),
+    "reng_hip_add_bf16_f32": (_I, [_P, _P, _SZ, _P, _P]),
 }
 
 
@@ -66,6 +71,14 @@ def lib():
     """Load libreng_hip.so (raises if it has not been built)."""
     global _lib
     if _lib is None:
+        # torch ships its own HIP runtime under the same soname; loading torch
+        # first makes libreng_hip.so bind to that one, so the process holds a
+        # single runtime (two runtimes on one device: the second to initialise
+        # finds no device).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise RengHipError(f"{LIB_PATH} is missing: build it with `make -C reciprocating-engine_amd`")
         L = ctypes.CDLL(LIB_PATH)
@@ -296,6 +309,58 @@ def gemm_fp8_scaled(a, a_fmt, scale_a, b, b_fmt, scale_b, M, N, K, out=None):
                                           na, _dev(b, "b"), _fmt(b_fmt),
                                           None if scale_b is None else _dev(scale_b, "sb"), nb, M, N, K,
                                           _dev(out, "out"), _stream()))
+    return out
+
+
+# ---------------------------------------------------------------- decode step
+# The non-GEMM steps of one Llama decoder layer at decode time (csrc/layer.hip);
+# the C++ host path (host/fp8_decoder.hpp) strings them together with the GEMV.
+
+
+def rms_norm_bf16(x, gamma, rows, cols, eps, out=None):
+    """out[rows, cols] bf16 = x / sqrt(mean(x^2) + eps) * gamma, x f32 (ops.rs:49-72)."""
+    import torch
+
+    if out is None:
+        out = torch.empty(rows * cols, dtype=torch.bfloat16, device=x.device)
+    _check(lib().reng_hip_rms_norm_bf16(_dev(x, "x"), _dev(gamma, "gamma"), rows, cols, eps, _dev(out, "out"),
+                                        _stream()))
+    return out
+
+
+def rope_append(q, k, v, n_heads, n_kv_heads, head_dim, sin_row, cos_row, k_row, v_row):
+    """Rotate-half RoPE of one position: q in place, k into k_row, v copied to v_row."""
+    _check(lib().reng_hip_rope_append(_dev(q, "q"), _dev(k, "k"), _dev(v, "v"), n_heads, n_kv_heads, head_dim,
+                                      _dev(sin_row, "sin_row"), _dev(cos_row, "cos_row"), _dev(k_row, "k_row"),
+                                      _dev(v_row, "v_row"), _stream()))
+
+
+def attention_decode(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, length, scale, out=None):
+    """One query per head over cache rows 0 .. length - 1, bf16 out [n_heads * head_dim]."""
+    import torch
+
+    if out is None:
+        out = torch.empty(n_heads * head_dim, dtype=torch.bfloat16, device=q.device)
+    _check(lib().reng_hip_attention_decode(_dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), n_heads,
+                                           n_kv_heads, head_dim, length, scale, _dev(out, "out"), _stream()))
+    return out
+
+
+def silu_mul_bf16(gate, up, n, out=None):
+    import torch
+
+    if out is None:
+        out = torch.empty(n, dtype=torch.bfloat16, device=gate.device)
+    _check(lib().reng_hip_silu_mul_bf16(_dev(gate, "gate"), _dev(up, "up"), n, _dev(out, "out"), _stream()))
+    return out
+
+
+def add_bf16_f32(x, d, n, out=None):
+    import torch
+
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=x.device)
+    _check(lib().reng_hip_add_bf16_f32(_dev(x, "x"), _dev(d, "d"), n, _dev(out, "out"), _stream()))
     return out
 
 

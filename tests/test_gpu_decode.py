@@ -1,0 +1,202 @@
+"""The device consumer of the fp8 codes: one decode step of a Llama decoder
+layer on the fp8 GEMVs (reng_model::Fp8Decoder, reciprocating-engine_amd/host/
+fp8_decoder.hpp; kernels csrc/layer.hip), the layer the reference refuses to
+run at crates/reng-model/src/lib.rs:2636-2649.
+
+Checked against the oracle's restatement of the reference's CPU decoder layer
+(oracle/layer.py: layer_cpu, crates/reng-synapse/src/model.rs:2903-3100,
+causal) over the same codes dequantized (the oracle's quantizer, bit-exact to
+the device's). Position p of the device decode must equal row p of the causal
+layer over positions 0 .. p.
+
+Tolerance: the device rounds every GEMV input and output to bf16 (the w8a16
+contract) where the reference layer stays f32, so the branch outputs
+(y - x) are held to relative L2 < 3e-2 and the layer output to < 1e-2.
+"""
+import json
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+import layer as L
+import oracle as O
+from helpers import bf16_bits, bf16_f32
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CPP = os.path.join(ROOT, "tests", "cpp")
+BIN = os.path.join(CPP, "build", "test_reng_decode")
+
+
+def _built():
+    if not os.path.exists(BIN):
+        subprocess.run(["make", "-C", CPP], check=True, capture_output=True)
+    return BIN
+
+
+def write_llama(d, hidden, inter, layers, heads, kv, vocab, theta, seed, sigma=0.06):
+    """A Llama checkpoint with gains near 1 and projections N(0, sigma), bf16;
+    returns the tensors as bf16 bit arrays."""
+    rng = np.random.default_rng(seed)
+    hd = hidden // heads
+    cfg = {"model_type": "llama", "hidden_size": hidden, "intermediate_size": inter,
+           "num_hidden_layers": layers, "num_attention_heads": heads, "num_key_value_heads": kv,
+           "rms_norm_eps": 1e-5, "vocab_size": vocab, "tie_word_embeddings": True, "rope_theta": theta}
+    with open(os.path.join(d, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    shapes = {"model.embed_tokens.weight": ((vocab, hidden), sigma), "model.norm.weight": ((hidden,), None)}
+    for i in range(layers):
+        p = f"model.layers.{i}."
+        shapes.update({
+            p + "input_layernorm.weight": ((hidden,), None), p + "post_attention_layernorm.weight": ((hidden,), None),
+            p + "self_attn.q_proj.weight": ((heads * hd, hidden), sigma),
+            p + "self_attn.k_proj.weight": ((kv * hd, hidden), sigma),
+            p + "self_attn.v_proj.weight": ((kv * hd, hidden), sigma),
+            p + "self_attn.o_proj.weight": ((hidden, heads * hd), sigma),
+            p + "mlp.gate_proj.weight": ((inter, hidden), sigma), p + "mlp.up_proj.weight": ((inter, hidden), sigma),
+            p + "mlp.down_proj.weight": ((hidden, inter), sigma),
+        })
+    tensors, header, data = {}, {}, bytearray()
+    for name, (shape, s) in shapes.items():
+        x = (1.0 + rng.standard_normal(shape) * 0.1) if s is None else rng.standard_normal(shape) * s
+        b = bf16_bits(x.astype(np.float32)).reshape(shape)
+        tensors[name] = b
+        raw = b.astype("<u2").tobytes()
+        header[name] = (shape, len(data), len(data) + len(raw))
+        data += raw
+    parts = [f'"{n}":{{"dtype":"BF16","shape":[{", ".join(map(str, s))}],"data_offsets":[{a},{b}]}}'
+             for n, (s, a, b) in header.items()]
+    h = ("{" + ",".join(parts) + "}").encode()
+    h += b" " * (-len(h) % 8)
+    with open(os.path.join(d, "model.safetensors"), "wb") as f:
+        f.write(struct.pack("<Q", len(h)) + h + bytes(data))
+    return tensors
+
+
+def oracle_layer_weights(t, li, fmt, scheme):
+    p = f"model.layers.{li}."
+    w = {"g1": bf16_f32(t[p + "input_layernorm.weight"]), "g2": bf16_f32(t[p + "post_attention_layernorm.weight"])}
+    for key, name in (("wq", "self_attn.q_proj"), ("wk", "self_attn.k_proj"), ("wv", "self_attn.v_proj"),
+                      ("wo", "self_attn.o_proj"), ("wg", "mlp.gate_proj"), ("wu", "mlp.up_proj"),
+                      ("wd", "mlp.down_proj")):
+        b = t[p + name + ".weight"]
+        rows, cols = b.shape
+        w[key] = O.quantize(b.ravel(), rows, cols, fmt, scheme).dequantize().reshape(rows, cols).astype(np.float32)
+    return w
+
+
+def test_decode_step_refusals(tmp_path):
+    write_llama(str(tmp_path), 64, 128, 2, 4, 2, 16, 10000.0, seed=1)
+    r = subprocess.run([_built(), "--refusals", str(tmp_path)], capture_output=True, text=True, timeout=60)
+    print(r.stdout)
+    assert r.returncode == 0 and "0 failed" in r.stdout, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("spec,fmt,scheme", [("e4m3:pcs", O.E4M3, "pcs"), ("e5m2:hw", O.E5M2, "hw")])
+def test_fp8_decode_step_matches_the_causal_cpu_layer(tmp_path, spec, fmt, scheme):
+    hidden, inter, layers, heads, kv, tokens, theta = 256, 512, 2, 8, 2, 12, 10000.0
+    hd = hidden // heads
+    t = write_llama(str(tmp_path), hidden, inter, layers, heads, kv, 32, theta, seed=7)
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    x.tofile(tmp_path / "in.f32")
+    r = subprocess.run([_built(), str(tmp_path), str(tmp_path / "in.f32"), str(tmp_path / "out.f32"), str(tokens),
+                        "--fp8", spec], capture_output=True, text=True, timeout=110)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    got = np.fromfile(tmp_path / "out.f32", dtype=np.float32).reshape(layers, tokens, hidden)
+    sin, cos = L.rope_caches(tokens, hd, theta)
+    for li in range(layers):
+        w = oracle_layer_weights(t, li, fmt, scheme)
+        want = L.layer(x, w, heads, kv, hd, 1e-5, sin, cos, hd ** -0.5)
+        branch = O.rel_l2((got[li] - x).ravel(), (want - x).ravel())
+        whole = O.rel_l2(got[li].ravel(), want.ravel())
+        print(f"layer {li}: branch rel_L2 {branch:.2e}, output rel_L2 {whole:.2e}")
+        assert branch < 3e-2 and whole < 1e-2
+        # Every position, not just on average.
+        for p in range(tokens):
+            assert O.rel_l2((got[li, p] - x[p]), (want[p] - x[p])) < 6e-2, (li, p)
+
+
+def test_decode_step_entry_points_refuse_bad_arguments():
+    """Refused before any device work (EINVAL), so no GPU is needed."""
+    import ctypes
+
+    import reng_hip as R
+
+    lib = R.lib()
+    p = ctypes.c_void_p(16)   # never dereferenced: every call here fails its checks first
+    assert lib.reng_hip_rms_norm_bf16(None, p, 1, 8, 1e-5, p, None) == R.EINVAL
+    assert lib.reng_hip_rms_norm_bf16(p, p, 0, 8, 1e-5, p, None) == R.EINVAL
+    assert lib.reng_hip_rms_norm_bf16(p, p, 1, 8, -1.0, p, None) == R.EINVAL
+    assert lib.reng_hip_rope_append(p, p, p, 6, 4, 64, p, p, p, p, None) == R.EINVAL       # 6 % 4
+    assert lib.reng_hip_rope_append(p, p, p, 4, 2, 63, p, p, p, p, None) == R.EINVAL       # odd head_dim
+    assert lib.reng_hip_attention_decode(p, p, p, 4, 2, 64, 0, 1.0, p, None) == R.EINVAL   # empty cache
+    assert lib.reng_hip_attention_decode(p, p, p, 4, 2, 64, 15001, 1.0, p, None) == R.EINVAL
+    assert b"cache length" in lib.reng_hip_last_error()
+    assert lib.reng_hip_attention_decode(ctypes.c_void_p(18), ctypes.c_void_p(18), p, 4, 2, 64, 3, 1.0, p,
+                                         None) == R.EINVAL                                # misaligned k_cache
+    assert lib.reng_hip_silu_mul_bf16(p, p, 0, p, None) == R.EINVAL
+    assert lib.reng_hip_add_bf16_f32(p, None, 4, p, None) == R.EINVAL
+
+
+@pytest.mark.gpu
+def test_decode_step_kernels_against_numpy():
+    import torch
+
+    import reng_hip as R
+
+    rng = np.random.default_rng(21)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    # RMSNorm over rows that are not a multiple of the block.
+    x = rng.standard_normal((3, 1000)).astype(np.float32) * 3
+    g = (1 + rng.standard_normal(1000) * 0.1).astype(np.float32)
+    got = bf16_f32(bits(R.rms_norm_bf16(dev(x), dev(g), 3, 1000, 1e-5))).reshape(3, 1000)
+    assert O.rel_l2(got.ravel(), L.rms_norm(x, g, 1e-5).ravel()) < 4e-3
+    # RoPE + append at position 5, 6 q heads over 2 kv heads.
+    nh, nkv, hd, pos = 6, 2, 64, 5
+    sin, cos = L.rope_caches(8, hd, 10000.0)
+    q = bf16_bits(rng.standard_normal(nh * hd).astype(np.float32))
+    k = bf16_bits(rng.standard_normal(nkv * hd).astype(np.float32))
+    v = bf16_bits(rng.standard_normal(nkv * hd).astype(np.float32))
+    dq = dev(q.view(np.int16))
+    kc = torch.zeros(8 * nkv * hd, dtype=torch.int16, device="cuda")
+    vc = torch.zeros_like(kc)
+    R.rope_append(dq, dev(k.view(np.int16)), dev(v.view(np.int16)), nh, nkv, hd, dev(sin[pos]), dev(cos[pos]),
+                  kc[pos * nkv * hd:], vc[pos * nkv * hd:])
+    want_q = L.rope(bf16_f32(q)[None, :], sin[pos:pos + 1], cos[pos:pos + 1], hd)[0]
+    want_k = L.rope(bf16_f32(k)[None, :], sin[pos:pos + 1], cos[pos:pos + 1], hd)[0]
+    assert O.rel_l2(bf16_f32(bits(dq)), want_q) < 4e-3
+    kcache = bf16_f32(bits(kc)).reshape(8, nkv * hd)
+    assert O.rel_l2(kcache[pos], want_k) < 4e-3
+    assert np.array_equal(bits(vc).reshape(8, nkv * hd)[pos], v)
+    assert not kcache[:pos].any() and not kcache[pos + 1:].any()
+    # Attention over 1 key is its value; over 700 keys against numpy softmax.
+    for length in (1, 700):
+        kb = bf16_bits(rng.standard_normal((length, nkv * hd)).astype(np.float32))
+        vb = bf16_bits(rng.standard_normal((length, nkv * hd)).astype(np.float32))
+        qb = bf16_bits(rng.standard_normal(nh * hd).astype(np.float32))
+        out = bf16_f32(bits(R.attention_decode(dev(qb.view(np.int16)), dev(kb.view(np.int16)), dev(vb.view(np.int16)),
+                                               nh, nkv, hd, length, hd ** -0.5)))
+        want = np.zeros(nh * hd, dtype=np.float32)
+        K, V, Q = bf16_f32(kb), bf16_f32(vb), bf16_f32(qb)
+        for h in range(nh):
+            gi = h // (nh // nkv)
+            s = K[:, gi * hd:(gi + 1) * hd] @ Q[h * hd:(h + 1) * hd] * hd ** -0.5
+            e = np.exp(s - s.max())
+            want[h * hd:(h + 1) * hd] = (e / e.sum()) @ V[:, gi * hd:(gi + 1) * hd]
+        if length == 1:
+            assert np.array_equal(bf16_bits(out), bf16_bits(want))
+        assert O.rel_l2(out, want) < 4e-3, length
+    # SiLU * up and the residual add.
+    gt = bf16_bits((rng.standard_normal(999) * 4).astype(np.float32))
+    up = bf16_bits(rng.standard_normal(999).astype(np.float32))
+    got = bf16_f32(bits(R.silu_mul_bf16(dev(gt.view(np.int16)), dev(up.view(np.int16)), 999)))
+    assert O.rel_l2(got, L.silu(bf16_f32(gt)) * bf16_f32(up)) < 4e-3
+    xr = rng.standard_normal(999).astype(np.float32)
+    out = R.add_bf16_f32(dev(xr), dev(up.view(np.int16)), 999).cpu().numpy()
+    assert np.array_equal(out, xr + bf16_f32(up))
