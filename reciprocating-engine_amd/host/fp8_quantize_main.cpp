@@ -3,12 +3,14 @@
 // and the relative error of the round trip. The same command line, output
 // and refusals as crates/reng-model/src/bin/fp8_quantize.rs:1-141.
 //
-//   reng-fp8-quantize <model_dir> [--fp8 <spec>] [--per-matrix] [--layers <n>]
+//   reng-fp8-quantize <model_dir> [--fp8 <spec>] [--per-matrix] [--layers <n>] [--save]
 //
 // <spec> is the value the RENG_FP8 switch takes: a format (e4m3, e5m2), a
 // scale scheme (pcs, hw, unit) and backoff=<f32>, colon- or comma-separated;
 // the default is e4m3:pcs. --per-matrix prints a line per matrix of the first
-// --layers layers (default 1) as well as the totals.
+// --layers layers (default 1) as well as the totals. --save, which the
+// reference does not have, also writes the codes and scales beside the
+// checkpoint (model.fp8.safetensors, read back by load_weights_fp8_cached).
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -21,12 +23,13 @@ using namespace reng_model;
 
 namespace {
 
-const char *USAGE = "usage: reng-fp8-quantize <model_dir> [--fp8 <spec>] [--per-matrix] [--layers <n>]";
+const char *USAGE = "usage: reng-fp8-quantize <model_dir> [--fp8 <spec>] [--per-matrix] [--layers <n>] [--save]";
 
 struct Args {
     std::string dir;
     Fp8Config fp8;
     bool per_matrix = false;
+    bool save = false;
     size_t layers = 1;
 };
 
@@ -48,6 +51,9 @@ Args parse_args(int argc, char **argv) {
     for (size_t i = 1; i < a.size();) {
         if (a[i] == "--per-matrix") {
             out.per_matrix = true;
+            i += 1;
+        } else if (a[i] == "--save") {
+            out.save = true;
             i += 1;
         } else if (a[i] == "--fp8") {
             if (i + 1 >= a.size()) throw Error(USAGE);
@@ -85,6 +91,10 @@ int run(int argc, char **argv) {
     const double after = (double)(report.fp8_bytes + report.scale_bytes);
     std::printf("projection bytes: %.3f GiB -> %.3f GiB (%.2fx, %.3f GiB saved)\n", report.bf16_bytes / gib,
                 after / gib, report.bf16_bytes / after, (report.bf16_bytes - after) / gib);
+    if (a.save) {
+        save_fp8(a.dir, w, a.fp8, report);
+        std::printf("saved %s/%s\n", a.dir.c_str(), FP8_CODES_FILE);
+    }
     if (a.per_matrix) {
         const auto &fp8 = *w.fp8;
         for (size_t li = 0; li < fp8.size() && li < a.layers; ++li) {

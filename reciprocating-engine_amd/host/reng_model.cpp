@@ -2,9 +2,11 @@
 #include "reng_model.hpp"
 
 #include <hip/hip_runtime_api.h>
+#include <sys/stat.h>
 
 #include <algorithm>
 #include <cctype>
+#include <cerrno>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -454,6 +456,166 @@ std::pair<LlamaWeights, std::optional<Fp8Report>> load_weights_fp8(const std::st
     if (!fp8) return {std::move(w), std::nullopt};
     const Fp8Report r = w.quantize_fp8(cfg, *fp8);
     return {std::move(w), r};
+}
+
+// ------------------------------------------------------------ fp8 codes on disk
+
+namespace {
+
+// The __metadata__ "format" value of a codes file, versioned with the layout.
+constexpr const char *FP8_CODES_FORMAT = "reng-fp8 codes 1";
+
+// "name size mtime_ns" of each file the weights come from, ';'-separated:
+// config.json, the shard index when there is one, then the checkpoint files.
+std::string source_fingerprint(const std::string &dir) {
+    std::vector<std::string> paths = {dir + "/config.json"};
+    struct stat st;
+    const std::string idx = dir + "/model.safetensors.index.json";
+    if (::stat((dir + "/model.safetensors").c_str(), &st) != 0 && ::stat(idx.c_str(), &st) == 0)
+        paths.push_back(idx);
+    const Checkpoint ck = Checkpoint::open(dir);
+    for (const std::string &f : ck.files()) paths.push_back(f);
+    std::string out;
+    for (const std::string &p : paths) {
+        if (::stat(p.c_str(), &st) != 0) throw Error("cannot stat " + p + ": " + std::strerror(errno));
+        const size_t slash = p.find_last_of('/');
+        const long long ns = (long long)st.st_mtim.tv_sec * 1000000000LL + (long long)st.st_mtim.tv_nsec;
+        out += (out.empty() ? "" : ";") + (slash == std::string::npos ? p : p.substr(slash + 1)) + " " +
+               std::to_string((unsigned long long)st.st_size) + " " + std::to_string(ns);
+    }
+    return out;
+}
+
+// The seven projections of one layer with the [rows, cols] the config implies.
+struct MatShape {
+    const char *name;
+    reng_fp8::Quantized *q;
+    size_t rows, cols;
+};
+
+std::vector<MatShape> layer_shapes(const LlamaConfig &cfg, LayerFp8 &l) {
+    const size_t h = cfg.hidden_size, i = cfg.intermediate_size, qd = cfg.q_dim();
+    const size_t kvd = cfg.n_kv_heads() * cfg.head_dim();
+    return {{"wq", &l.wq, qd, h}, {"wk", &l.wk, kvd, h}, {"wv", &l.wv, kvd, h}, {"wo", &l.wo, h, qd},
+            {"wg", &l.wg, i, h},  {"wu", &l.wu, i, h},   {"wd", &l.wd, h, i}};
+}
+
+}  // namespace
+
+void save_fp8(const std::string &dir, const LlamaWeights &w, const Fp8Config &q, const Fp8Report &r) {
+    if (!w.fp8) throw Error("save_fp8: the weights carry no fp8 codes");
+    std::map<std::string, std::string> meta;
+    meta["format"] = FP8_CODES_FORMAT;
+    meta["fp8"] = q.to_string();
+    meta["source"] = source_fingerprint(dir);
+    meta["layers"] = std::to_string(w.fp8->size());
+    meta["matrices"] = std::to_string(r.matrices);
+    meta["bf16_bytes"] = std::to_string(r.bf16_bytes);
+    meta["fp8_bytes"] = std::to_string(r.fp8_bytes);
+    meta["scale_bytes"] = std::to_string(r.scale_bytes);
+    meta["mean_rel"] = f32_shortest(r.mean_rel);
+    meta["max_rel"] = f32_shortest(r.max_rel);
+    char secs[32];
+    std::snprintf(secs, sizeof secs, "%.6f", r.secs);
+    meta["secs"] = secs;
+    // Scales first, then codes: every F32 tensor starts 4-byte aligned.
+    std::vector<TensorOut> scales, codes;
+    for (size_t li = 0; li < w.fp8->size(); ++li)
+        for (const auto &m : (*w.fp8)[li].matrices()) {
+            const reng_fp8::Quantized &x = *m.second;
+            if (x.codes.size() != x.rows * x.cols || x.scales.size() != x.rows)
+                throw Error("save_fp8: layer " + std::to_string(li) + " " + m.first + " is not [rows, cols]");
+            if (x.format != q.format || x.scaling != q.scaling)
+                throw Error("save_fp8: layer " + std::to_string(li) + " " + m.first + " was not made with " +
+                            q.to_string());
+            const std::string p = "layers." + std::to_string(li) + "." + m.first;
+            meta[p + ".exp_bias"] = std::to_string(x.exp_bias);
+            scales.push_back({p + ".scales", "F32", {x.rows}, x.scales.data(), x.scales.size() * 4});
+            codes.push_back({p + ".codes", "U8", {x.rows, x.cols}, x.codes.data(), x.codes.size()});
+        }
+    scales.insert(scales.end(), codes.begin(), codes.end());
+    write_safetensors(dir + "/" + FP8_CODES_FILE, scales, meta);
+}
+
+std::optional<Fp8Report> load_fp8(const std::string &dir, const LlamaConfig &cfg, LlamaWeights &w,
+                                  const Fp8Config &q) {
+    const auto t0 = std::chrono::steady_clock::now();
+    const std::string path = dir + "/" + FP8_CODES_FILE;
+    struct stat st;
+    if (::stat(path.c_str(), &st) != 0) return std::nullopt;
+    const Checkpoint f = Checkpoint::open_file(path);
+    const auto &meta = f.metadata();
+    auto get = [&](const std::string &key) -> const std::string & {
+        auto it = meta.find(key);
+        if (it == meta.end()) throw Error(path + ": no " + key + " in the metadata");
+        return it->second;
+    };
+    auto number = [&](const std::string &key) -> unsigned long long {
+        const std::string &v = get(key);
+        char *end = nullptr;
+        const unsigned long long n = std::strtoull(v.c_str(), &end, 10);
+        if (v.empty() || *end != '\0' || v[0] == '-') throw Error(path + ": " + key + " " + v + " is not a count");
+        return n;
+    };
+    auto real = [&](const std::string &key) -> double {
+        const std::string &v = get(key);
+        char *end = nullptr;
+        const double x = std::strtod(v.c_str(), &end);
+        if (v.empty() || *end != '\0') throw Error(path + ": " + key + " " + v + " is not a number");
+        return x;
+    };
+    auto fmt = meta.find("format");
+    if (fmt == meta.end() || fmt->second != FP8_CODES_FORMAT)
+        throw Error(path + " is not an fp8 codes file (" + FP8_CODES_FORMAT + ")");
+    if (get("fp8") != q.to_string() || get("source") != source_fingerprint(dir)) return std::nullopt;
+    if (number("layers") != cfg.num_hidden_layers)
+        throw Error(path + ": " + get("layers") + " layers, the config has " + std::to_string(cfg.num_hidden_layers));
+    std::vector<LayerFp8> out(cfg.num_hidden_layers);
+    for (size_t li = 0; li < out.size(); ++li)
+        for (const MatShape &m : layer_shapes(cfg, out[li])) {
+            const std::string p = "layers." + std::to_string(li) + "." + m.name;
+            const TensorInfo &ci = f.info(p + ".codes");
+            const TensorInfo &si = f.info(p + ".scales");
+            if (ci.dtype != Dtype::U8 || ci.shape != std::vector<size_t>{m.rows, m.cols})
+                throw Error(path + ": " + p + ".codes is " + ci.dtype_name + " of the wrong shape, expected U8 " +
+                            shape_debug(m.rows, m.cols));
+            if (si.dtype != Dtype::F32 || si.shape != std::vector<size_t>{m.rows})
+                throw Error(path + ": " + p + ".scales is " + si.dtype_name + " of the wrong shape, expected F32 [" +
+                            std::to_string(m.rows) + "]");
+            const unsigned long long eb = number(p + ".exp_bias");
+            if (eb > 0xffffffffULL) throw Error(path + ": " + p + ".exp_bias " + std::to_string(eb) + " is out of range");
+            m.q->format = q.format;
+            m.q->scaling = q.scaling;
+            m.q->rows = m.rows;
+            m.q->cols = m.cols;
+            m.q->codes = f.u8(p + ".codes");
+            m.q->scales = f.f32(p + ".scales");
+            m.q->exp_bias = (uint32_t)eb;
+        }
+    Fp8Report r;
+    r.matrices = number("matrices");
+    r.bf16_bytes = number("bf16_bytes");
+    r.fp8_bytes = number("fp8_bytes");
+    r.scale_bytes = number("scale_bytes");
+    r.mean_rel = (float)real("mean_rel");
+    r.max_rel = (float)real("max_rel");
+    w.fp8 = std::move(out);
+    r.secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    return r;
+}
+
+Fp8Load load_weights_fp8_cached(const std::string &dir, const LlamaConfig &cfg, std::optional<Fp8Config> fp8,
+                                bool save) {
+    Fp8Load out;
+    out.weights = load_weights(dir, cfg);
+    if (!fp8) return out;
+    if ((out.report = load_fp8(dir, cfg, out.weights, *fp8))) {
+        out.from_file = true;
+        return out;
+    }
+    out.report = out.weights.quantize_fp8(cfg, *fp8);
+    if (save) save_fp8(dir, out.weights, *fp8, *out.report);
+    return out;
 }
 
 }  // namespace reng_model

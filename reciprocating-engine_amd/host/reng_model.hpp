@@ -127,6 +127,42 @@ LlamaWeights load_weights(const std::string &dir, const LlamaConfig &cfg);
 std::pair<LlamaWeights, std::optional<Fp8Report>> load_weights_fp8(const std::string &dir, const LlamaConfig &cfg,
                                                                    std::optional<Fp8Config> fp8);
 
+// ------------------------------------------------------------ fp8 codes on disk
+//
+// The reference quantizes at every load (lib.rs:1871-1876, 1955-1966). These
+// keep one quantization pass beside the checkpoint instead, as a safetensors
+// file of U8 code and F32 scale tensors ("layers.<i>.<wq|wk|wv|wo|wg|wu|wd>.
+// codes" [rows, cols], ".scales" [rows]) whose __metadata__ holds the switch
+// that made them, each matrix's exp_bias, the quantization report and a
+// fingerprint (name, size and modification time) of config.json and of every
+// checkpoint file the weights were read from.
+
+// The file's name in the model directory.
+constexpr const char *FP8_CODES_FILE = "model.fp8.safetensors";
+
+// Writes w.fp8 (made by quantize_fp8 with the switch q, which reported r) to
+// dir/FP8_CODES_FILE through a temporary file and a rename. Throws Error when
+// w carries no fp8 codes or on an I/O failure.
+void save_fp8(const std::string &dir, const LlamaWeights &w, const Fp8Config &q, const Fp8Report &r);
+
+// Reads dir/FP8_CODES_FILE into w.fp8 and returns the report saved with the
+// codes (secs: the time this read took) when the file exists, was made with
+// the switch q, and its fingerprint matches the directory's files now;
+// nullopt, w untouched, otherwise. Throws Error for a current file whose
+// tensors do not have the shapes cfg implies or which is not such a file.
+std::optional<Fp8Report> load_fp8(const std::string &dir, const LlamaConfig &cfg, LlamaWeights &w,
+                                  const Fp8Config &q);
+
+// load_weights_fp8 that takes the codes from dir/FP8_CODES_FILE when load_fp8
+// finds them current, and otherwise quantizes and, if save, writes the file.
+struct Fp8Load {
+    LlamaWeights weights;
+    std::optional<Fp8Report> report;
+    bool from_file = false;
+};
+Fp8Load load_weights_fp8_cached(const std::string &dir, const LlamaConfig &cfg, std::optional<Fp8Config> fp8,
+                                bool save);
+
 // The shortest decimal that reads back as the same f32 (Rust's {} for f32).
 std::string f32_shortest(float x);
 

@@ -44,6 +44,7 @@ size_t dtype_size(Dtype d) {
         case Dtype::BF16:
         case Dtype::F16: return 2;
         case Dtype::F32: return 4;
+        case Dtype::U8: return 1;
         default: return 0;
     }
 }
@@ -200,7 +201,12 @@ void Checkpoint::add_file(const std::string &path, const std::map<std::string, b
     const size_t data0 = 8 + (size_t)hlen, data_len = map->size() - data0;
     const size_t shard = files_.size();
     for (const auto &kv : h.obj) {
-        if (kv.first == "__metadata__") continue;
+        if (kv.first == "__metadata__") {
+            if (kv.second.kind == reng_json::Value::Object)
+                for (const auto &m : kv.second.obj)
+                    if (m.second.kind == reng_json::Value::String) metadata_[m.first] = m.second.str;
+            continue;
+        }
         if (only && !only->count(kv.first)) continue;
         const reng_json::Value &t = kv.second;
         TensorInfo ti;
@@ -219,6 +225,7 @@ void Checkpoint::add_file(const std::string &path, const std::map<std::string, b
         ti.dtype = ti.dtype_name == "BF16" ? Dtype::BF16
                    : ti.dtype_name == "F16" ? Dtype::F16
                    : ti.dtype_name == "F32" ? Dtype::F32
+                   : ti.dtype_name == "U8"  ? Dtype::U8
                                             : Dtype::Other;
         if (ti.begin > ti.end || ti.end > data_len)
             throw Error("safetensors: " + fname + ": tensor " + kv.first + ": data outside the file");
@@ -234,6 +241,7 @@ void Checkpoint::add_file(const std::string &path, const std::map<std::string, b
         tensors_[kv.first] = ti;
     }
     files_.push_back(std::move(map));
+    paths_.push_back(path);
 }
 
 const TensorInfo &Checkpoint::info(const std::string &name) const {
@@ -304,6 +312,78 @@ std::vector<float> Checkpoint::f32(const std::string &name) const {
         default: throw Error("tensor " + name + ": unsupported dtype " + t.dtype_name);
     }
     return out;
+}
+
+std::vector<uint8_t> Checkpoint::u8(const std::string &name) const {
+    const TensorInfo &t = info(name);
+    if (t.dtype != Dtype::U8) throw Error("tensor " + name + ": " + t.dtype_name + ", expected U8");
+    const uint8_t *p = files_[t.shard]->data() + t.begin;
+    return std::vector<uint8_t>(p, p + (t.end - t.begin));
+}
+
+namespace {
+
+std::string json_string(const std::string &v) {
+    std::string o = "\"";
+    for (unsigned char ch : v) {
+        if (ch == '"' || ch == '\\') {
+            o += '\\';
+            o += (char)ch;
+        } else if (ch < 0x20) {
+            char b[8];
+            std::snprintf(b, sizeof b, "\\u%04x", ch);
+            o += b;
+        } else {
+            o += (char)ch;
+        }
+    }
+    return o + "\"";
+}
+
+}  // namespace
+
+void write_safetensors(const std::string &path, const std::vector<TensorOut> &tensors,
+                       const std::map<std::string, std::string> &metadata) {
+    std::string header = "{";
+    if (!metadata.empty()) {
+        header += "\"__metadata__\":{";
+        bool first = true;
+        for (const auto &m : metadata) {
+            header += (first ? "" : ",") + json_string(m.first) + ":" + json_string(m.second);
+            first = false;
+        }
+        header += "}";
+    }
+    size_t off = 0;
+    for (size_t i = 0; i < tensors.size(); ++i) {
+        const TensorOut &t = tensors[i];
+        const Dtype d = t.dtype == "BF16" ? Dtype::BF16 : t.dtype == "F16" ? Dtype::F16
+                        : t.dtype == "F32" ? Dtype::F32 : t.dtype == "U8" ? Dtype::U8 : Dtype::Other;
+        size_t n = 1;
+        for (size_t x : t.shape) n *= x;
+        if (d == Dtype::Other || n * dtype_size(d) != t.bytes)
+            throw Error("safetensors: tensor " + t.name + ": " + std::to_string(t.bytes) + " bytes for " + t.dtype +
+                        " " + shape_str(t.shape));
+        header += std::string(header.size() > 1 ? "," : "") + json_string(t.name) + ":{\"dtype\":\"" + t.dtype +
+                  "\",\"shape\":" + shape_str(t.shape) + ",\"data_offsets\":[" + std::to_string(off) + "," +
+                  std::to_string(off + t.bytes) + "]}";
+        off += t.bytes;
+    }
+    header += "}";
+    while (header.size() % 8 != 0) header.push_back(' ');
+    const std::string tmp = path + ".tmp";
+    FILE *f = std::fopen(tmp.c_str(), "wb");
+    if (!f) throw Error("cannot write " + tmp + ": " + std::strerror(errno));
+    uint8_t len[8];
+    for (int i = 0; i < 8; ++i) len[i] = (uint8_t)((uint64_t)header.size() >> (8 * i));
+    bool ok = std::fwrite(len, 1, 8, f) == 8 && std::fwrite(header.data(), 1, header.size(), f) == header.size();
+    for (const TensorOut &t : tensors)
+        ok = ok && (t.bytes == 0 || std::fwrite(t.data, 1, t.bytes, f) == t.bytes);
+    ok = (std::fclose(f) == 0) && ok;
+    if (!ok || std::rename(tmp.c_str(), path.c_str()) != 0) {
+        std::remove(tmp.c_str());
+        throw Error("cannot write " + path + ": " + std::strerror(errno));
+    }
 }
 
 Bf16Slice Checkpoint::linear(const std::string &name, size_t out_dim, size_t in_dim) const {

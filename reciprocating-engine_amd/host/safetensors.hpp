@@ -73,7 +73,7 @@ private:
     bool mapped_ = false;
 };
 
-enum class Dtype { BF16, F16, F32, Other };
+enum class Dtype { BF16, F16, F32, U8, Other };
 
 struct TensorInfo {
     std::string name;
@@ -103,12 +103,35 @@ public:
     std::vector<float> f32(const std::string &name) const;
     // A [out, in] linear weight, shape-checked (lib.rs:1361-1370).
     Bf16Slice linear(const std::string &name, size_t out_dim, size_t in_dim) const;
+    // A U8 tensor's bytes.
+    std::vector<uint8_t> u8(const std::string &name) const;
+    // The string entries of the files' __metadata__ objects.
+    const std::map<std::string, std::string> &metadata() const { return metadata_; }
+    // The files the tensors come from, in the order they were opened.
+    const std::vector<std::string> &files() const { return paths_; }
 
 private:
     void add_file(const std::string &path, const std::map<std::string, bool> *only);
     std::vector<std::shared_ptr<const Mapping>> files_;
     std::map<std::string, TensorInfo> tensors_;
+    std::map<std::string, std::string> metadata_;
+    std::vector<std::string> paths_;
 };
+
+// One tensor for write_safetensors: dtype "BF16", "F16", "F32" or "U8"; bytes
+// must be the shape's element count times the element size.
+struct TensorOut {
+    std::string name, dtype;
+    std::vector<size_t> shape;
+    const void *data = nullptr;
+    size_t bytes = 0;
+};
+
+// Writes a safetensors file (tensors in the given order, no holes, header
+// padded to 8 bytes, metadata as the header's __metadata__ strings) to
+// path + ".tmp" and renames it over path. Throws Error on an I/O failure.
+void write_safetensors(const std::string &path, const std::vector<TensorOut> &tensors,
+                       const std::map<std::string, std::string> &metadata);
 
 // bf16 / f16 helpers shared by the loader.
 float f16_to_f32(uint16_t h);

@@ -3,10 +3,12 @@
 //
 //   test_reng_decode --refusals <model_dir>
 //       (host only) the configurations the decode step refuses, each with its message
-//   test_reng_decode <model_dir> <in.f32> <out.f32> <tokens> [--fp8 <spec>]
+//   test_reng_decode <model_dir> <in.f32> <out.f32> <tokens> [--fp8 <spec>] [--cached]
 //       loads the checkpoint with the fp8 switch on, runs every layer over
 //       positions 0 .. tokens - 1 on the rows of in ([tokens, hidden] f32) and
-//       writes out ([layers, tokens, hidden] f32)
+//       writes out ([layers, tokens, hidden] f32); --cached takes the codes
+//       from the model directory's saved codes file and fails if it is not
+//       current
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -82,17 +84,34 @@ std::vector<float> read_f32(const std::string &path, size_t n) {
 int main(int argc, char **argv) {
     try {
         if (argc == 3 && std::string(argv[1]) == "--refusals") return refusals(argv[2]);
-        if (argc != 5 && argc != 7) {
-            std::fprintf(stderr, "usage: test_reng_decode <model_dir> <in.f32> <out.f32> <tokens> [--fp8 <spec>]\n");
+        std::optional<Fp8Config> fp8 = Fp8Config{};
+        bool cached = false, usage = argc < 5;
+        for (int i = 5; i < argc && !usage; ++i) {
+            const std::string a = argv[i];
+            if (a == "--fp8" && i + 1 < argc) fp8 = fp8_switch(std::string_view(argv[++i]), true);
+            else if (a == "--cached") cached = true;
+            else usage = true;
+        }
+        if (usage) {
+            std::fprintf(stderr,
+                         "usage: test_reng_decode <model_dir> <in.f32> <out.f32> <tokens> [--fp8 <spec>] [--cached]\n");
             return 2;
         }
         const std::string dir = argv[1];
         const size_t tokens = std::strtoull(argv[4], nullptr, 10);
-        std::optional<Fp8Config> fp8 = Fp8Config{};
-        if (argc == 7) fp8 = fp8_switch(std::string_view(argv[6]), true);
         const LlamaConfig cfg = LlamaConfig::load(dir);
-        auto [w, report] = load_weights_fp8(dir, cfg, fp8);
-        if (report) std::printf("%s\n", report->to_string().c_str());
+        Fp8Load loaded;
+        if (cached) {
+            loaded = load_weights_fp8_cached(dir, cfg, fp8, false);
+            if (!loaded.from_file) throw Error(std::string("no current ") + FP8_CODES_FILE + " in " + dir);
+            std::printf("codes from %s\n", FP8_CODES_FILE);
+        } else {
+            auto [fresh, report] = load_weights_fp8(dir, cfg, fp8);
+            loaded.weights = std::move(fresh);
+            loaded.report = report;
+        }
+        const LlamaWeights &w = loaded.weights;
+        if (loaded.report) std::printf("%s\n", loaded.report->to_string().c_str());
         Fp8Decoder dec(cfg, w, tokens);
         const size_t hidden = cfg.hidden_size;
         const std::vector<float> in = read_f32(argv[2], tokens * hidden);

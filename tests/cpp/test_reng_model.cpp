@@ -6,6 +6,7 @@
 //
 //   test_reng_model [--cpu-only] [NAME_SUBSTRING]
 #include <dirent.h>
+#include <fcntl.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -151,6 +152,44 @@ LlamaConfig write_tiny_llama(const std::string &dir) {
     }
     write_file(dir + "/model.safetensors", safetensors_bytes(ts));
     return LlamaConfig::load(dir);
+}
+
+// w.fp8 as the oracle quantizes w's projections with q (host only), and the
+// report of that pass with made-up error figures.
+Fp8Report oracle_fp8(const LlamaConfig &cfg, LlamaWeights &w, const Fp8Config &q) {
+    (void)cfg;
+    Fp8Report r;
+    std::vector<LayerFp8> out(w.layers.size());
+    for (size_t l = 0; l < w.layers.size(); ++l) {
+        const LayerTensors &t = w.layers[l];
+        const Bf16Slice *src[7] = {&t.wq, &t.wk, &t.wv, &t.wo, &t.wg, &t.wu, &t.wd};
+        reng_fp8::Quantized *dst[7] = {&out[l].wq, &out[l].wk, &out[l].wv, &out[l].wo,
+                                       &out[l].wg, &out[l].wu, &out[l].wd};
+        const size_t hid = cfg.hidden_size, inter = cfg.intermediate_size, qd = cfg.q_dim();
+        const size_t kvd = cfg.n_kv_heads() * cfg.head_dim();
+        const size_t rows[7] = {qd, kvd, kvd, hid, inter, inter, hid};
+        for (size_t k = 0; k < 7; ++k) {
+            reng_fp8::Quantized &x = *dst[k];
+            x.format = q.format;
+            x.scaling = q.scaling;
+            x.rows = rows[k];
+            x.cols = src[k]->size() / rows[k];
+            x.codes.resize(x.rows * x.cols);
+            x.scales.resize(x.rows);
+            const std::vector<uint16_t> wv = src[k]->to_vector();
+            x.exp_bias = orc_quantize_with(wv.data(), x.rows, x.cols, (int)q.format, (int)q.scaling, q.backoff,
+                                           x.codes.data(), x.scales.data(), 8);
+            r.matrices += 1;
+            r.bf16_bytes += wv.size() * 2;
+            r.fp8_bytes += x.codes.size();
+            r.scale_bytes += x.scales.size() * 4;
+        }
+    }
+    r.mean_rel = 0.0123f;
+    r.max_rel = 0.0456f;
+    r.secs = 1.5;
+    w.fp8 = std::move(out);
+    return r;
 }
 
 // ------------------------------------------------------------------ host-only
@@ -357,6 +396,80 @@ void the_fp8_switch_on_quantizes_the_projections_and_nothing_else() {
     expect(line.rfind("7 matrices, 0.00 GiB bf16 -> 0.00 GiB fp8 + 0 KiB scales, mean rel ", 0) == 0, line);
 }
 
+// save_fp8 / load_fp8: the file reads back bit-for-bit, goes stale when the
+// switch or a source file changes, and refuses tensors of the wrong shape and
+// files of another kind.
+void fp8_codes_file_round_trips_and_goes_stale() {
+    TempDir d;
+    const LlamaConfig cfg = write_tiny_llama(d.path);
+    const Fp8Config q = fp8_switch(std::string_view("e5m2:pcs:backoff=0.75"), true).value();
+    LlamaWeights w = load_weights(d.path, cfg);
+    expect_throws([&] { save_fp8(d.path, w, q, Fp8Report{}); }, "carry no fp8 codes", "save without codes");
+    const Fp8Report r = oracle_fp8(cfg, w, q);
+    LlamaWeights none = load_weights(d.path, cfg);
+    expect(!load_fp8(d.path, cfg, none, q).has_value() && !none.fp8, "no file: nullopt");
+    save_fp8(d.path, w, q, r);
+    struct stat st;
+    expect(stat((d.path + "/" + FP8_CODES_FILE).c_str(), &st) == 0, "file written");
+    expect(stat((d.path + "/" + FP8_CODES_FILE + ".tmp").c_str(), &st) != 0, "no temporary left");
+
+    LlamaWeights back = load_weights(d.path, cfg);
+    const auto got = load_fp8(d.path, cfg, back, q);
+    expect(got.has_value() && back.fp8 && back.fp8->size() == 1, "current file loads");
+    expect(got->matrices == r.matrices && got->bf16_bytes == r.bf16_bytes && got->fp8_bytes == r.fp8_bytes &&
+               got->scale_bytes == r.scale_bytes && got->mean_rel == r.mean_rel && got->max_rel == r.max_rel,
+           "report fields");
+    const auto a = (*w.fp8)[0].matrices(), b = (*back.fp8)[0].matrices();
+    for (size_t k = 0; k < a.size(); ++k) {
+        const reng_fp8::Quantized &x = *a[k].second, &y = *b[k].second;
+        const std::string what = a[k].first;
+        expect(x.rows == y.rows && x.cols == y.cols, what + ": shape");
+        expect(x.format == y.format && x.scaling == y.scaling && x.exp_bias == y.exp_bias, what + ": scheme");
+        expect(x.codes == y.codes, what + ": codes");
+        expect(std::memcmp(x.scales.data(), y.scales.data(), x.rows * 4) == 0 && y.scales.size() == x.rows,
+               what + ": scales");
+    }
+    auto cached = load_weights_fp8_cached(d.path, cfg, q, false);
+    expect(cached.from_file && cached.report && cached.weights.fp8, "cached load takes the file");
+    expect((*cached.weights.fp8)[0].wd.codes == (*w.fp8)[0].wd.codes, "cached codes");
+    auto off = load_weights_fp8_cached(d.path, cfg, std::nullopt, false);
+    expect(!off.from_file && !off.report && !off.weights.fp8, "switch off: no codes");
+
+    // Another switch: stale.
+    LlamaWeights other = load_weights(d.path, cfg);
+    expect(!load_fp8(d.path, cfg, other, Fp8Config{}).has_value() && !other.fp8, "another switch is stale");
+    // A source file touched: stale.
+    const std::string cfg_path = d.path + "/config.json";
+    struct timespec ts[2] = {{0, UTIME_OMIT}, {1000000000, 0}};
+    expect(utimensat(AT_FDCWD, cfg_path.c_str(), ts, 0) == 0, "utimensat");
+    expect(!load_fp8(d.path, cfg, other, q).has_value() && !other.fp8, "touched config is stale");
+    expect(utimensat(AT_FDCWD, (d.path + "/model.safetensors").c_str(), ts, 0) == 0, "utimensat");
+    save_fp8(d.path, w, q, r);
+    expect(load_fp8(d.path, cfg, other, q).has_value(), "saved again: current");
+    ts[1].tv_sec += 1;
+    expect(utimensat(AT_FDCWD, (d.path + "/model.safetensors").c_str(), ts, 0) == 0, "utimensat");
+    other.fp8.reset();
+    expect(!load_fp8(d.path, cfg, other, q).has_value() && !other.fp8, "touched checkpoint is stale");
+
+    // A current file whose wg is not [intermediate, hidden].
+    LlamaWeights bad = w;
+    (*bad.fp8)[0].wg.rows = 8;
+    (*bad.fp8)[0].wg.codes.resize(8 * 8);
+    (*bad.fp8)[0].wg.scales.resize(8);
+    save_fp8(d.path, bad, q, r);
+    expect_throws([&] { (void)load_fp8(d.path, cfg, other, q); }, "layers.0.wg.codes is U8 of the wrong shape",
+                  "wrong shape");
+    expect(!other.fp8, "w untouched on a refusal");
+    // Codes made with another switch than the one named.
+    expect_throws([&] { save_fp8(d.path, w, Fp8Config{}, r); }, "was not made with", "switch mismatch");
+    // Another kind of safetensors file under the name.
+    const uint8_t one = 1;
+    write_safetensors(d.path + "/" + FP8_CODES_FILE, {{"x", "U8", {1}, &one, 1}}, {{"format", "other"}});
+    expect_throws([&] { (void)load_fp8(d.path, cfg, other, q); }, "is not an fp8 codes file", "other file");
+    expect_throws([&] { write_safetensors(d.path + "/x.safetensors", {{"x", "F32", {2}, &one, 1}}, {}); },
+                  "1 bytes for F32 [2]", "writer checks sizes");
+}
+
 // A larger random model, every scheme: each projection's codes, scales and
 // bias against the oracle, and the report's error statistics against the
 // oracle's sample_row_errors.
@@ -533,6 +646,7 @@ const Test TESTS[] = {
     {"safetensors_views_convert_and_refuse", false, safetensors_views_convert_and_refuse},
     {"a_sharded_checkpoint_loads_through_its_index", false, a_sharded_checkpoint_loads_through_its_index},
     {"the_fp8_switch_off_leaves_the_weights_bf16", false, the_fp8_switch_off_leaves_the_weights_bf16},
+    {"fp8_codes_file_round_trips_and_goes_stale", false, fp8_codes_file_round_trips_and_goes_stale},
     {"the_fp8_switch_on_quantizes_the_projections_and_nothing_else", true,
      the_fp8_switch_on_quantizes_the_projections_and_nothing_else},
     {"quantize_fp8_matches_the_oracle_on_every_matrix", true, quantize_fp8_matches_the_oracle_on_every_matrix},
@@ -549,6 +663,20 @@ const Test TESTS[] = {
 }  // namespace
 
 int main(int argc, char **argv) {
+    // --save-codes <model_dir> <spec>: the oracle's codes for the checkpoint
+    // written with save_fp8 (host only), for a reader outside this library.
+    if (argc == 4 && std::string(argv[1]) == "--save-codes") {
+        try {
+            const LlamaConfig cfg = LlamaConfig::load(argv[2]);
+            const Fp8Config q = fp8_switch(std::string_view(argv[3]), true).value();
+            LlamaWeights w = load_weights(argv[2], cfg);
+            save_fp8(argv[2], w, q, oracle_fp8(cfg, w, q));
+            return 0;
+        } catch (const std::exception &e) {
+            std::fprintf(stderr, "Error: %s\n", e.what());
+            return 1;
+        }
+    }
     bool cpu_only = false;
     std::string filter;
     for (int i = 1; i < argc; ++i) {

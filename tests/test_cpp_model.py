@@ -5,12 +5,16 @@ compares every quantized projection with the oracle; the CLI is run here as the
 reference's bin/fp8_quantize.rs would be. Without a GPU only the host side
 runs (the switch grammar, the config, the safetensors loader, the CLI's
 refusals)."""
+import json
 import os
 import struct
 import subprocess
 
 import numpy as np
 import pytest
+from safetensors import safe_open
+
+import oracle as O
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CPP = os.path.join(ROOT, "tests", "cpp")
@@ -76,7 +80,7 @@ def write_checkpoint(d, hidden=64, inter=160, layers=2, heads=4, kv=2, vocab=32,
 
 def test_model_slice_host_side():
     out = _run("--cpu-only", timeout=120)
-    assert "9 run, 0 failed" in out
+    assert "10 run, 0 failed" in out
 
 
 def test_cli_refusals(tmp_path):
@@ -153,3 +157,82 @@ def test_probe_timing_gate():
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "speedup-4096x14336-m1" in r.stdout and "PASS" in r.stdout
+
+
+MATS = ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
+HF = {"wq": "self_attn.q_proj", "wk": "self_attn.k_proj", "wv": "self_attn.v_proj", "wo": "self_attn.o_proj",
+      "wg": "mlp.gate_proj", "wu": "mlp.up_proj", "wd": "mlp.down_proj"}
+
+
+def _bf16_tensors(path):
+    """The BF16 tensors of a safetensors file as uint16 arrays (numpy has no
+    bfloat16, so the safetensors library cannot hand them over)."""
+    raw = open(path, "rb").read()
+    n = struct.unpack("<Q", raw[:8])[0]
+    header = json.loads(raw[8:8 + n])
+    out = {}
+    for name, t in header.items():
+        if name != "__metadata__" and t["dtype"] == "BF16":
+            a, b = t["data_offsets"]
+            out[name] = np.frombuffer(raw[8 + n + a:8 + n + b], dtype="<u2").reshape(t["shape"])
+    return out
+
+
+def check_codes_file(d, spec, fmt, scheme, backoff, layers):
+    """The codes file beside the checkpoint, read with the safetensors library:
+    its layout (F32 scales, then U8 codes, no holes), its metadata, and every
+    matrix's codes, scales and exp_bias against the oracle's quantize_with of
+    the checkpoint's bf16 weights."""
+    path = os.path.join(d, "model.fp8.safetensors")
+    src = _bf16_tensors(os.path.join(d, "model.safetensors"))
+    raw = open(path, "rb").read()
+    n = struct.unpack("<Q", raw[:8])[0]
+    assert n % 8 == 0
+    header = json.loads(raw[8:8 + n])
+    spans = sorted((t["data_offsets"], t["dtype"]) for k, t in header.items() if k != "__metadata__")
+    assert spans[0][0][0] == 0 and spans[-1][0][1] == len(raw) - 8 - n
+    assert all(a[0][1] == b[0][0] for a, b in zip(spans, spans[1:])), "holes between tensors"
+    assert [dt for _, dt in spans] == ["F32"] * (7 * layers) + ["U8"] * (7 * layers)
+    with safe_open(path, framework="np") as f:
+        meta = f.metadata()
+        assert meta["format"] == "reng-fp8 codes 1" and meta["fp8"] == spec
+        assert meta["layers"] == str(layers) and int(meta["matrices"]) == 7 * layers
+        assert set(meta["source"].split(";")[0].split()[:1]) == {"config.json"}
+        for li in range(layers):
+            for m in MATS:
+                w = src[f"model.layers.{li}.{HF[m]}.weight"]
+                rows, cols = w.shape
+                q = O.quantize_with(w, rows, cols, fmt, scheme, backoff)
+                codes = f.get_tensor(f"layers.{li}.{m}.codes")
+                scales = f.get_tensor(f"layers.{li}.{m}.scales")
+                assert codes.dtype == np.uint8 and codes.shape == (rows, cols)
+                assert scales.dtype == np.float32 and scales.shape == (rows,)
+                assert np.array_equal(codes.ravel(), q.codes), (li, m, "codes")
+                assert np.array_equal(scales.view(np.uint32), q.scales.view(np.uint32)), (li, m, "scales")
+                assert int(meta[f"layers.{li}.{m}.exp_bias"]) == q.exp_bias, (li, m, "exp_bias")
+
+
+def test_codes_file_reads_with_the_safetensors_library(tmp_path):
+    """save_fp8's file (the oracle's codes, written by the host library) is a
+    safetensors file any reader takes, with the codes where it says."""
+    write_checkpoint(str(tmp_path))
+    r = subprocess.run([_built(BIN, CPP), "--save-codes", str(tmp_path), "e5m2:hw:backoff=0.5"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    check_codes_file(str(tmp_path), "e5m2/hw backoff 0.5", O.E5M2, "hw", 0.5, layers=2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("spec,name,fmt,scheme,backoff", [
+    ("e4m3:pcs", "e4m3/pcs backoff 1", O.E4M3, "pcs", 1.0),
+    ("e5m2:unit", "e5m2/unit backoff 1", O.E5M2, "unit", 1.0),
+    ("hw:backoff=0.25", "e4m3/hw backoff 0.25", O.E4M3, "hw", 0.25),
+])
+def test_cli_saves_the_device_codes(tmp_path, spec, name, fmt, scheme, backoff):
+    """reng-fp8-quantize --save: the device quantizer's codes on disk equal
+    the oracle's bit for bit."""
+    write_checkpoint(str(tmp_path))
+    r = _cli(str(tmp_path), "--fp8", spec, "--save")
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.splitlines()[-1] == f"saved {tmp_path}/model.fp8.safetensors"
+    check_codes_file(str(tmp_path), name, fmt, scheme, backoff, layers=2)

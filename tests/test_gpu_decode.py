@@ -121,6 +121,38 @@ def test_fp8_decode_step_matches_the_causal_cpu_layer(tmp_path, spec, fmt, schem
             assert O.rel_l2((got[li, p] - x[p]), (want[p] - x[p])) < 6e-2, (li, p)
 
 
+@pytest.mark.gpu
+def test_decode_from_saved_codes_equals_the_fresh_quantize(tmp_path):
+    """Codes written by reng-fp8-quantize --save and read back by
+    load_weights_fp8_cached decode to the same bits as a fresh quantize."""
+    hidden, inter, layers, heads, kv, tokens = 256, 512, 2, 8, 2, 6
+    write_llama(str(tmp_path), hidden, inter, layers, heads, kv, 32, 10000.0, seed=3)
+    x = np.random.default_rng(5).standard_normal((tokens, hidden)).astype(np.float32)
+    x.tofile(tmp_path / "in.f32")
+    def run(out, *extra, spec="e5m2:pcs"):
+        return subprocess.run([_built(), str(tmp_path), str(tmp_path / "in.f32"), str(tmp_path / out), str(tokens),
+                               "--fp8", spec, *extra], capture_output=True, text=True, timeout=110)
+
+    r = run("fresh.f32", "--cached")
+    assert r.returncode == 1 and "no current model.fp8.safetensors" in r.stderr
+    r = run("fresh.f32")
+    assert r.returncode == 0, r.stdout + r.stderr
+    cli = os.path.join(ROOT, "reciprocating-engine_amd", "bin", "reng-fp8-quantize")
+    env = {k: v for k, v in os.environ.items() if k != "RENG_FP8"}
+    r = subprocess.run([cli, str(tmp_path), "--fp8", "e5m2:pcs", "--save"], capture_output=True, text=True,
+                       timeout=110, env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    r = run("cached.f32", "--cached")
+    print(r.stdout)
+    assert r.returncode == 0 and "codes from model.fp8.safetensors" in r.stdout, r.stdout + r.stderr
+    fresh = np.fromfile(tmp_path / "fresh.f32", dtype=np.uint32)
+    cached = np.fromfile(tmp_path / "cached.f32", dtype=np.uint32)
+    assert fresh.size == layers * tokens * hidden and np.array_equal(fresh, cached)
+    # Another switch does not take the saved codes.
+    r = run("other.f32", "--cached", spec="e4m3:pcs")
+    assert r.returncode == 1 and "no current model.fp8.safetensors" in r.stderr
+
+
 def test_decode_step_entry_points_refuse_bad_arguments():
     """Refused before any device work (EINVAL), so no GPU is needed."""
     import ctypes
