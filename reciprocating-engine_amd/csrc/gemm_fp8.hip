@@ -6,7 +6,9 @@
 // v_mfma_f32_32x32x64_f8f6f4 on the OCP fp8 formats, whose finite codes
 // 0x00-0x77 (e4m3) / 0x00-0x7b (e5m2) mean exactly what reng-fp8's codes mean.
 //
-// Block = 2 x 2 waves; a wave owns WM x WN tiles of 32 x 32, so the block tile
+// Two kernels: gemm_fp8_wide (further down) for shapes of whole 256 x 256 /
+// 256 x 128 tiles, and gemm_fp8_mfma for everything else. gemm_fp8_mfma:
+// block = 2 x 2 waves; a wave owns WM x WN tiles of 32 x 32, so the block tile
 // is BM = 64 WM by BN = 64 WN. A pipeline stage covers BK = 64 KS codes of k.
 // Each stage's operand rows are copied global -> LDS by the waves'
 // global_load_lds_dwordx4 (1 KB per instruction, no VGPR staging) into an
@@ -318,6 +320,214 @@ int launch_fp8_cfg(const Fp8Args &g, hipStream_t st) {
     return check_launch("gemm_fp8_mfma");
 }
 
+// ------------------------------------------------------------ wide tiles
+//
+// The large-output form: 8 waves (2 x 4, two per SIMD) over a BM x BN tile of
+// 256 x 256 or 256 x 128, K in 128-code stages. A wave owns WM x WN MFMA
+// tiles (4 x 2: 128 x 64 outputs, or 4 x 1). The operand copies are
+// buffer_load_dwordx4 ... lds through a buffer resource: the per-lane part of
+// the address (row within the copy, swizzled chunk) is one VGPR for every
+// copy of the wave, and the copy's row base and k offset ride in the scalar
+// soffset, so the copy addresses cost no registers. Only shapes that divide
+// into whole tiles take this form (every row read exists; no clamping).
+// Two waves per SIMD let one wave's MFMAs run while the other waits on its
+// fragment reads or the stage barrier; the 256 x 256 tile halves the operand
+// bytes each output needs against 128 x 128.
+
+constexpr int WIDE_WAVES = 8;
+
+__device__ __forceinline__ void copy16_buf(__amdgpu_buffer_rsrc_t r, uint8_t *l, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)l, 16, voff, soff, 0, 0);
+}
+
+template <int WM, int WN>
+struct WideTile {
+    static constexpr int WGM = 2, WGN = 4;   // wave grid
+    static constexpr int BM = 32 * WM * WGM, BN = 32 * WN * WGN, BK = 128;
+    static constexpr int CH = BK / 16, ROWS = 1024 / BK;   // 8 chunks per LDS row, 8 rows per 1 KB copy
+    static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE = A_BYTES + B_BYTES;
+    static constexpr int LA = BM / ROWS / WIDE_WAVES, LB = BN / ROWS / WIDE_WAVES;   // copies per wave per stage
+    static constexpr int LOADS = LA + LB;
+    static_assert(LA * ROWS * WIDE_WAVES == BM && LB * ROWS * WIDE_WAVES == BN, "copies split evenly");
+};
+
+template <int FA, int FB, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *__restrict__ a,
+                                                                const float *__restrict__ sa, uint32_t nsa,
+                                                                const uint8_t *__restrict__ b,
+                                                                const float *__restrict__ sb, uint32_t nsb, uint32_t M,
+                                                                uint32_t N, uint32_t K, uint32_t tiles_m,
+                                                                uint32_t tiles, uint16_t *__restrict__ out) {
+    using T = WideTile<WM, WN>;
+    constexpr int BM = T::BM, BN = T::BN, BK = T::BK, CH = T::CH, ROWS = T::ROWS, KS = BK / FK;
+    static_assert(S >= 2, "at least double-buffered");
+    static_assert((S - 1) * T::LOADS < 64, "vmcnt range");
+    static_assert(WM % 2 == 0, "the last k-step splits the wave's rows in two");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * T::STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / T::WGN, wn = wave % T::WGN;
+
+    // XCD-major tile order, m fastest (as gemm_fp8_mfma).
+    const uint32_t x = blockIdx.x % XCDS, l = blockIdx.x / XCDS;
+    const uint32_t per = tiles / XCDS, rem = tiles % XCDS;
+    const uint32_t tile = x * per + (x < rem ? x : rem) + l;
+    const uint32_t m0 = (tile % tiles_m) * BM, n0 = (tile / tiles_m) * BN;
+    const uint32_t n = K / BK;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)a, 0, M * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)b, 0, N * K, 0x00020000);
+    // Lane part of a copy: tile row (copy base) + lane / CH, the chunk that
+    // lands in slot lane % CH. The swizzle reads the row's low five bits and a
+    // copy's base is a multiple of ROWS, so there are 32 / ROWS lane parts.
+    constexpr int VAR = 32 / ROWS;
+    uint32_t voff[VAR];
+#pragma unroll
+    for (int v = 0; v < VAR; ++v)
+        voff[v] = (uint32_t)(lane / CH) * K + (((lane % CH) ^ swz<CH>(v * ROWS + lane / CH)) * 16);
+    auto issue = [&](uint32_t step, int slot) {
+        uint8_t *base = lds + slot * T::STAGE;
+        const uint32_t ko = step * BK;
+#pragma unroll
+        for (int q = 0; q < T::LA; ++q) {
+            const uint32_t c = wave * T::LA + q, tr0 = c * ROWS;
+            copy16_buf(ra, base + tr0 * BK, voff[c % VAR], (m0 + tr0) * K + ko);
+        }
+#pragma unroll
+        for (int q = 0; q < T::LB; ++q) {
+            const uint32_t c = wave * T::LB + q, tr0 = c * ROWS;
+            copy16_buf(rb, base + T::A_BYTES + tr0 * BK, voff[c % VAR], (n0 + tr0) * K + ko);
+        }
+    };
+    auto clampi = [&](uint32_t i) { return i < n ? i : n - 1; };
+
+    const uint32_t rl = lane & 31, h = lane >> 5, sw = swz<CH>(rl);
+    auto read_frags = [&](int slot, int ks, i32x8 (&fa)[WM], i32x8 (&fb)[WN]) {
+        const uint8_t *base = lds + slot * T::STAGE;
+        const uint32_t o0 = ((4 * ks + 2 * h) ^ sw) * 16, o1 = ((4 * ks + 2 * h + 1) ^ sw) * 16;
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const uint8_t *p = base + (wm * (32 * WM) + i * 32 + rl) * BK;
+            const u32x4 x0 = *reinterpret_cast<const u32x4 *>(p + o0);
+            const u32x4 x1 = *reinterpret_cast<const u32x4 *>(p + o1);
+            fa[i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        }
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const uint8_t *p = base + T::A_BYTES + (wn * (32 * WN) + j * 32 + rl) * BK;
+            const u32x4 x0 = *reinterpret_cast<const u32x4 *>(p + o0);
+            const u32x4 x1 = *reinterpret_cast<const u32x4 *>(p + o1);
+            fb[j] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        }
+    };
+
+    f32x16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    auto mfma_rows = [&](int i0, int i1, const i32x8 (&fa)[WM], const i32x8 (&fb)[WN]) {
+#pragma unroll
+        for (int i = i0; i < i1; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], FB, FA, 0, 0,
+                                                                            0, 0);
+    };
+
+    // The pipeline of gemm_fp8_mfma: S stages in flight from the prologue;
+    // per stage one barrier after each wave's own copies of the next stage
+    // have landed, then the copy of stage t + S into the slot stage t used.
+#pragma unroll
+    for (int s = 0; s < S; ++s) issue(clampi(s), s);
+    wait_vmcnt<(S - 1) * T::LOADS>();
+    lds_barrier();
+    i32x8 fa[2][WM], fb[2][WN];
+    read_frags(0, 0, fa[0], fb[0]);
+    auto kstep = [&](auto cur_c, auto ks_c, uint32_t t) {
+        constexpr int CUR = decltype(cur_c)::value, NXT = CUR ^ 1, KSI = decltype(ks_c)::value;
+        if constexpr (KSI + 1 < KS) {
+            read_frags((int)(t % S), KSI + 1, fa[NXT], fb[NXT]);
+            mfma_rows(0, WM, fa[CUR], fb[CUR]);
+            interleave<WM * WN, 2 * (WM + WN), 0>();
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            mfma_rows(0, WM / 2, fa[CUR], fb[CUR]);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<(S - 2) * T::LOADS>();
+            lds_barrier();
+            issue(clampi(t + S), (int)(t % S));
+            read_frags((int)((t + 1) % S), 0, fa[NXT], fb[NXT]);
+            mfma_rows(WM / 2, WM, fa[CUR], fb[CUR]);
+            interleave<WM / 2 * WN, 2 * (WM + WN), T::LOADS>();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    static_assert(KS == 2, "two k-steps per stage");
+    uint32_t t = 0;
+    for (; t + 1 < n; t += 2) {
+        kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
+        kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t);
+        kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t + 1);
+        kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t + 1);
+    }
+    if (t < n) {
+        kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
+        kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t);
+    }
+    wait_vmcnt<0>();   // the clamped surplus copies land before LDS is released
+
+    // Epilogue: lane l holds output row m0 + ... + l % 32 and, per group g of
+    // four accumulators, four consecutive columns; one 8-byte store each.
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        const uint32_t m = m0 + wm * (32 * WM) + i * 32 + rl;
+        const float sam = nsa == 0 ? 1.0f : (nsa == 1 ? sa[0] : sa[m]);
+        uint16_t *orow = out + (size_t)m * N;
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t nb = n0 + wn * (32 * WN) + j * 32 + 8 * g + 4 * h;
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sbn = nsb == 0 ? 1.0f : (nsb == 1 ? sb[0] : sb[nb + e]);
+                    o[e] = acc[i][j][4 * g + e] * sam * sbn;
+                }
+                const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
+                const uint32_t hi = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
+                *reinterpret_cast<u32x2 *>(orow + nb) = u32x2{lo, hi};
+            }
+    }
+}
+
+// Whether the wide (WM, WN) form takes this product: whole tiles, K in whole
+// stages, byte offsets in 31 bits, 8-byte aligned output rows.
+template <int WM, int WN>
+bool wide_fits(const Fp8Args &g) {
+    using T = WideTile<WM, WN>;
+    return g.M % T::BM == 0 && g.N % T::BN == 0 && g.K % T::BK == 0 && (uint64_t)g.M * g.K < (1ull << 31) &&
+           (uint64_t)g.N * g.K < (1ull << 31) && reinterpret_cast<uintptr_t>(g.out) % 8 == 0;
+}
+
+template <int WM, int WN, int S>
+int launch_fp8_wide(const Fp8Args &g, hipStream_t st) {
+    using T = WideTile<WM, WN>;
+    const uint32_t tiles_m = g.M / T::BM, tiles = tiles_m * (g.N / T::BN);
+#define RENG_FP8_WIDE(A, B)                                                                                      \
+    hipLaunchKernelGGL((gemm_fp8_wide<A, B, WM, WN, S>), dim3(tiles), dim3(64 * WIDE_WAVES), 0, st, g.a, g.sa, \
+                       g.nsa, g.b, g.sb, g.nsb, g.M, g.N, g.K, tiles_m, tiles, g.out)
+    if (g.fa == RENG_HIP_E4M3 && g.fb == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 0);
+    else if (g.fa == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 1);
+    else if (g.fb == RENG_HIP_E4M3) RENG_FP8_WIDE(1, 0);
+    else RENG_FP8_WIDE(1, 1);
+#undef RENG_FP8_WIDE
+    return check_launch("gemm_fp8_wide");
+}
+
 }  // namespace fp8gemm
 
 int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, const uint8_t *b, int fb,
@@ -331,6 +541,12 @@ int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, con
     const uint64_t cus = (uint64_t)device_props().cus;
     const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
     const uint64_t t128 = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+    const uint64_t t256x128 = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
+    // Whole 256 x 256 / 256 x 128 tiles: the 8-wave form, measured 10-17%
+    // faster on the M = 1024 prefill shapes than the 4-wave tiles below
+    // (256 x 128 with three stages once 256 x 256 tiles no longer fill the CUs).
+    if (t256 >= cus && wide_fits<4, 2>(g)) return launch_fp8_wide<4, 2, 2>(g, st);
+    if (t256 < cus && 2 * t256x128 >= cus && wide_fits<4, 1>(g)) return launch_fp8_wide<4, 1, 3>(g, st);
     if (t256 >= cus) return launch_fp8_cfg<4, 4, 2, 2>(g, st);
     if (t128 >= cus) return K > 8192 ? launch_fp8_cfg<4, 2, 2, 3>(g, st) : launch_fp8_cfg<2, 2, 2, 2>(g, st);
     if (K > 8192 && 2 * t128 >= cus) return launch_fp8_cfg<4, 2, 2, 3>(g, st);

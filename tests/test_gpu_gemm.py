@@ -227,6 +227,17 @@ def test_fp8_gemm_ragged_tiles(R, M, N, K):
     check_fp8(R, rng, M, N, K, E4M3, E4M3, sample_cols=160)
 
 
+# Whole-tile shapes take the 8-wave form: 256 x 256 tiles when they fill the
+# CUs (1024 x 16384), 256 x 128 otherwise (512 x 16384, 256 x 32768); K of one,
+# two and three 128-code stages, every format pair and scale form.
+@pytest.mark.parametrize("M,N,K", [(1024, 16384, 256), (512, 16384, 384), (256, 32768, 128)])
+@pytest.mark.parametrize("fa,fb", [(E4M3, E4M3), (E5M2, E5M2), (E4M3, E5M2), (E5M2, E4M3)])
+def test_fp8_gemm_wide_tiles(R, M, N, K, fa, fb):
+    rng = np.random.default_rng(M + N + K + 4 * fa + fb)
+    for act, nsb in (("pcs", "N"), ("unit", "1"), ("pcs", "0")):
+        check_fp8(R, rng, M, N, K, fa, fb, act, nsb, sample_cols=96)
+
+
 @pytest.mark.parametrize("shape", [(5120, 5120), (1024, 5120), (27648, 5120), (5120, 27648)])
 def test_fp8_gemm_prefill_qwen_32b_shapes(R, shape):
     rng = np.random.default_rng(127)
