@@ -1,9 +1,10 @@
 // gemm.hip - consumers of the quantizer's codes on CDNA4 (gfx950).
 //
-// 1. gemv_w8a16     (M <= 4): y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]).
+// 1. gemv_w8a16     (M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
+//                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]).
 //    Streams the codes once with 16-byte loads, decodes in registers
 //    (v_cvt_pk_f32_fp8 / _bf8), f32 FMA, one wave per output row.
-// 2. 4 < M <= 64: the same product on bf16 MFMA with the codes and the
+// 2. The other M <= 64: the same product on bf16 MFMA with the codes and the
 //    activation staged through LDS (skinny.hip); larger M in tiles of 64.
 // (The fp8 x fp8 product of gemm_fp8_scaled is in gemm_fp8.hip.)
 //
@@ -253,6 +254,12 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
         }
         return RENG_HIP_OK;
     }
+    // Three or four rows, or two once the activation outgrows the GEMV's LDS
+    // copy: the MFMA kernel (activation rows padded to 8) is faster than the
+    // GEMV's per-row dot products (Qwen2.5-7B [3584, 18944]: M = 3 26.3 ->
+    // 16.6 us, M = 2 22.5 -> 16.6 us; M = 2 with a short K stays on the GEMV).
+    if (M >= 2 && M <= 4 && K % 128 == 0 && (M >= 3 || (size_t)M * K * 2 > 64 * 1024))
+        return launch_skinny_mfma(x, codes, scales, M, N, K, F, y, st);
     if (M <= 4) {
         // Rows divide evenly over the waves: at most 16 waves per CU, each
         // taking rows_per_wave rows.

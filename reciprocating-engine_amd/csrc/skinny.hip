@@ -573,7 +573,7 @@ int launch_wide_f(const uint16_t *x, const uint8_t *codes, const float *scales, 
 
 }  // namespace skinny
 
-// 4 < M <= 16, K % 128 == 0.
+// 2 <= M <= 16, K % 128 == 0 (rows past M repeat row M - 1 and are not stored).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st) {
     using namespace skinny;

@@ -101,9 +101,13 @@ def test_gemv_batch1_llama_8b_shapes(R, fmt, shape):
 
 @pytest.mark.parametrize("M", [2, 3, 4])
 def test_gemv_small_batches(R, M):
+    """K % 128 != 0 keeps M <= 4 on the GEMV; with K % 128 == 0, M = 3 and 4
+    (and M = 2 at a long K) take the MFMA kernel with padded rows."""
     rng = np.random.default_rng(103 + M)
     check_w8a16(R, rng, M, 1024, 4096, E4M3)
+    check_w8a16(R, rng, M, 1024, 4112, E4M3)
     check_w8a16(R, rng, M, 100, 176, E5M2)
+    check_w8a16(R, rng, M, 300, 18944, E5M2)
 
 
 @pytest.mark.parametrize("M", [1, 3])
