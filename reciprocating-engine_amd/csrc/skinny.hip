@@ -98,20 +98,23 @@ __device__ __forceinline__ void lds_barrier() {
 // +16) of a chunk (g = l / 16; k-steps 0, 1 and 2, 3), decoded to bf16 in
 // registers (exact), and the activation row l % 16 at the same k. At the end
 // the KW partial tiles of a row group meet in LDS and are added in kw order.
-template <int F, int MA, int NT, int KW, int NW, int S>
+template <int F, int MA, int NT, int KW, int NW, int S, int ACTK>
 __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ codes,
                                                             const float *__restrict__ scales, uint32_t M,
                                                             uint32_t N, uint32_t K, uint16_t *__restrict__ y) {
     constexpr int TILE = 16 * STAGE_K;               // one 16-row tile of a stage, bytes
-    constexpr int WBYTES = NT * TILE, ABYTES = MA * STAGE_K * 2;
+    constexpr bool AR = ACTK > 0;                    // activation resident in LDS (K <= ACTK chunks)
+    constexpr int WBYTES = NT * TILE, ABYTES = AR ? 0 : MA * STAGE_K * 2;
     constexpr int SLOT = WBYTES + ABYTES, RING = S * SLOT;
-    constexpr int CA = MA / 2, C = 4 * NT + CA;      // copies per stage
+    constexpr int CA = AR ? 0 : MA / 2, C = 4 * NT + CA;   // copies per stage
+    constexpr int ACT_BYTES = ACTK * MA * CHUNK * 2;       // [chunk][MA rows][256 B]
     static_assert(S >= 2 && (S - 1) * C < 64, "pipeline depth");
     constexpr int W = KW * NW;
     constexpr int RED = KW > 1 ? W * NT * 1024 : 0;
-    constexpr int LDS = W * RING > RED ? W * RING : RED;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
+    constexpr int LDS0 = W * RING > RED ? W * RING : RED;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS0 + ACT_BYTES];
+    uint8_t *act = lds + LDS0;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -139,7 +142,7 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
             wsrc[t][i] = codes + (size_t)n * K + (size_t)c0 * CHUNK + (p >> 3) * CHUNK + (p & 7) * 16;
             whi |= (p >> 3) << (4 * t + i);
         }
-    const uint16_t *asrc[CA];
+    const uint16_t *asrc[CA > 0 ? CA : 1];
     uint32_t ahi = 0;
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
@@ -179,6 +182,7 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
         const bool half = one_chunk(st);
         const uint8_t *slot = ring + (st % S) * SLOT;
         const uint8_t *arow = slot + WBYTES + am * (STAGE_K * 2);
+        const uint32_t cc = c0 + 2 * st;   // the stage's first chunk
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             if (h == 1 && half) break;
@@ -192,8 +196,14 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
             u32x4 a[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t p = 16 * h + 2 * g + (j & 1) + 8 * (j >> 1);
-                a[j] = *reinterpret_cast<const u32x4 *>(arow + ((p ^ (am & 15)) * 16));
+                if constexpr (AR) {
+                    const uint32_t p = 2 * g + (j & 1) + 8 * (j >> 1);   // piece within chunk cc + h
+                    a[j] = *reinterpret_cast<const u32x4 *>(act + ((cc + h) * MA + am) * (CHUNK * 2) +
+                                                            ((p ^ (am & 15)) * 16));
+                } else {
+                    const uint32_t p = 16 * h + 2 * g + (j & 1) + 8 * (j >> 1);
+                    a[j] = *reinterpret_cast<const u32x4 *>(arow + ((p ^ (am & 15)) * 16));
+                }
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -219,10 +229,27 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
             sc[t][e] = scales ? scales[n < N ? n : N - 1] : 1.0f;
         }
 
+    if constexpr (AR) {
+        // The whole activation, once per block: chunk-major, row r's 16-byte
+        // piece p of a chunk in slot p ^ (r % 16); copies of 4 rows x 256 B
+        // spread over the waves, issued before any weight copy.
+        constexpr uint32_t PER = MA / 4;   // copies per chunk
+        for (uint32_t q = wave; q < chunks * PER; q += W) {
+            const uint32_t ch = q / PER, r0 = 4 * (q % PER), rr = r0 + (lane >> 4);
+            const uint32_t p = (lane & 15) ^ (rr & 15);
+            const uint32_t m = rr < M ? rr : M - 1;
+            copy16(reinterpret_cast<const uint8_t *>(x + (size_t)m * K + (size_t)ch * CHUNK + p * 8),
+                   act + (ch * MA + r0) * (CHUNK * 2));
+        }
+    }
     if (c0 < c1) {
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
             if ((uint32_t)s < nst) copies(s);
+        if constexpr (AR) {
+            wait_vmcnt<0>();   // this wave's activation copies (and first stages) have landed
+            lds_barrier();     // ... and every other wave's
+        }
         for (uint32_t st = 0; st < nst; ++st) {
             if (st + S - 1 < nst) {
                 wait_lgkm0();                // slot (st - 1) % S has been read
@@ -282,19 +309,22 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
     }
 }
 
-template <int F, int MA, int NT, int KW, int NW, int S>
+template <int F, int MA, int NT, int KW, int NW, int S, int ACTK = 0>
 int launch_cfg(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N, uint32_t K,
                uint16_t *y, hipStream_t st) {
     const uint32_t rows = 16 * NT * NW;
     const uint32_t blocks = (N + rows - 1) / rows;
-    hipLaunchKernelGGL((skinny_rows<F, MA, NT, KW, NW, S>), dim3(blocks), dim3(64 * KW * NW), 0, st, x, codes,
+    hipLaunchKernelGGL((skinny_rows<F, MA, NT, KW, NW, S, ACTK>), dim3(blocks), dim3(64 * KW * NW), 0, st, x, codes,
                        scales, M, N, K, y);
     return check_launch("skinny_rows");
 }
 
-// One block per CU at these LDS sizes (96-144 KB), so the grid is sized for a
-// single round: the fewest rows per block (16, 32, 64 or 128) whose grid fits
-// on the CUs; narrow blocks split K over their waves.
+// One block per CU at these LDS sizes (96-160 KB), so the grid is sized for a
+// single round: the fewest rows per block (16, 32, 64, 80 or 128) whose grid
+// fits on the CUs; narrow blocks split K over their waves. The 80-row form
+// (5 waves of 16 rows, M <= 8, K <= 4096) holds the activation in LDS for the
+// whole block instead of copying it per stage; on [18944, 3584] it keeps 237
+// CUs busy where 128-row blocks keep 148 (M = 8: 16.7 -> 14.8 us).
 template <int F, int MA>
 int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N, uint32_t K,
               uint16_t *y, hipStream_t st) {
@@ -306,6 +336,10 @@ int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint
     }
     if ((N + 31) / 32 <= cus) return launch_cfg<F, MA, 2, 4, 1, 2>(x, codes, scales, M, N, K, y, st);
     if ((N + 63) / 64 <= cus) return launch_cfg<F, MA, 2, 2, 2, S3>(x, codes, scales, M, N, K, y, st);
+    if constexpr (MA == 8) {
+        if ((N + 79) / 80 <= cus && K / CHUNK <= 32)
+            return launch_cfg<F, MA, 1, 1, 5, 3, 32>(x, codes, scales, M, N, K, y, st);
+    }
     return launch_cfg<F, MA, 2, 1, 4, S3>(x, codes, scales, M, N, K, y, st);
 }
 

@@ -136,12 +136,14 @@ def test_skinny_gemm_ragged_batches(R, M):
     check_w8a16(R, rng, M, 48, 4096, E5M2)
 
 
-# 4 < M <= 16 (skinny_rows): every block shape the launcher picks (16, 32, 64
-# or 128 rows per block by N), K runs with a one-chunk last stage (K % 256 ==
-# 128), K shorter than the waves' split (some waves get no chunk), N not a
-# multiple of 16 or of 4, and both staged-activation heights (8 and 16 rows).
+# 4 < M <= 16 (skinny_rows): every block shape the launcher picks (16, 32, 64,
+# 80 or 128 rows per block by N; the 80-row form holds the activation in LDS
+# for M <= 8 and K <= 4096: N = 20000, and 18950 at that K limit), K runs with
+# a one-chunk last stage (K % 256 == 128), K shorter than the waves' split
+# (some waves get no chunk), N not a multiple of 16 or of 4, and both
+# staged-activation heights (8 and 16 rows).
 @pytest.mark.parametrize("M", [5, 7, 8, 9, 12, 16])
-@pytest.mark.parametrize("N,K", [(200, 128), (4101, 384), (8000, 256), (16000, 3712), (20000, 1152)])
+@pytest.mark.parametrize("N,K", [(200, 128), (4101, 384), (8000, 256), (16000, 3712), (20000, 1152), (18950, 4096)])
 def test_skinny_rows_block_shapes(R, M, N, K):
     rng = np.random.default_rng(1000 * M + N + K)
     fmt = E4M3 if (M + N) % 2 else E5M2
