@@ -107,26 +107,29 @@ def time_quantize(torch, R, ws, fmt, steps, warmup):
     launches = ws.launches()
     batches = [[(m[4], m[2], m[3], m[5], m[6], m[7]) for m in chunk] for _, chunk, _ in launches]
 
+    # One event before a step's first launch and one after each launch: the
+    # launches run back to back on the stream, so launch i spans the event
+    # before it to the event after it (half the markers of a start/end pair
+    # per launch, each of which is a packet in the queue between kernels).
     def step(evs=None):
+        if evs is not None:
+            evs[0].record()
         for i, b in enumerate(batches):
-            if evs is not None:
-                evs[i][0].record()
             R.quantize_batch(b, fmt, "pcs", 1.0)
             if evs is not None:
-                evs[i][1].record()
+                evs[i + 1].record()
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in batches]
-           for _ in range(steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(batches) + 1)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(steps):
         step(evs[s])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_launch = [[a.elapsed_time(b) * 1e-3 for a, b in e] for e in evs]
+    per_launch = [[e[i].elapsed_time(e[i + 1]) * 1e-3 for i in range(len(batches))] for e in evs]
     step_s = wall / steps
     # The dominant kernel: the configuration carrying the most bytes per step.
     by_cfg = {}
