@@ -585,13 +585,27 @@ int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales
     return check_launch("reduce_splits");
 }
 
+// The (tiles, splits) launch_wide_cfg makes for R-row blocks.
+inline uint32_t wide_blocks(uint32_t N, uint32_t K, uint32_t R) {
+    const uint32_t tiles = (N + R - 1) / R, chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
+    const uint32_t max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
+    uint32_t splits = cus / tiles;
+    splits = splits < 1 ? 1 : splits > max_splits ? max_splits : splits;
+    return tiles * splits;
+}
+
 template <int F, int MT>
 int launch_wide_mt(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                    uint32_t K, uint16_t *y, hipStream_t st) {
     // 64-row blocks for small matrices (fewer splits: the partials cost more
     // than the activation re-reads there), else 128 (half the activation
-    // bytes per code).
+    // bytes per code) - unless 128-row blocks leave over 30% of the CUs idle
+    // and 96-row ones cover more (Qwen2.5-7B gate/up [18944, 3584]: 148 ->
+    // 198 blocks, M = 64: 26.8 -> 24.1 us).
     if ((uint64_t)N * K <= (16ull << 20)) return launch_wide_cfg<F, MT, 2, 6>(x, codes, scales, M, N, K, y, st);
+    const uint32_t cus = (uint32_t)device_props().cus, b128 = wide_blocks(N, K, 128);
+    if (10 * b128 < 7 * cus && wide_blocks(N, K, 96) > b128)
+        return launch_wide_cfg<F, MT, 3, 3>(x, codes, scales, M, N, K, y, st);
     return launch_wide_cfg<F, MT, 4, 4>(x, codes, scales, M, N, K, y, st);
 }
 

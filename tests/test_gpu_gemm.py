@@ -150,11 +150,14 @@ def test_skinny_rows_block_shapes(R, M, N, K):
     check_w8a16(R, rng, M, N, K, fmt, sample_cols=None if N * K <= 4096 * 384 else 512)
 
 
-# 16 < M <= 64 (skinny_wide): 64- and 128-row blocks, one K split (N past a
-# grid's worth of tiles) and many (the partials and their ordered reduce), the
-# scalar paths for N % 4 != 0, N below one block, 2, 3 and 4 activation tiles.
+# 16 < M <= 64 (skinny_wide): 64-, 96- and 128-row blocks (96 where 128-row
+# blocks leave CUs idle: N = 18950, K = 1024, with a partial last block), one K
+# split (N past a grid's worth of tiles) and many (the partials and their
+# ordered reduce), the scalar paths for N % 4 != 0, N below one block, 2, 3
+# and 4 activation tiles.
 @pytest.mark.parametrize("M", [17, 32, 40, 48, 63, 64])
-@pytest.mark.parametrize("N,K", [(48, 4096), (3584, 1152), (4101, 384), (40000, 256), (6000, 2944)])
+@pytest.mark.parametrize("N,K", [(48, 4096), (3584, 1152), (4101, 384), (40000, 256), (6000, 2944),
+                                 (18950, 1024)])
 def test_skinny_wide_block_shapes(R, M, N, K):
     rng = np.random.default_rng(2000 * M + N + K)
     fmt = E5M2 if (M + N) % 2 else E4M3
