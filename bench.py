@@ -34,9 +34,11 @@ sys.path.insert(0, os.path.join(ROOT, "reciprocating-engine_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 METRIC = "quantize GB/s; fp8 GEMV/GEMM % HBM/MFMA roofline, 8B shapes b1-b64"
-HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
-FP8_PEAK = 5.0e15            # MI355X dense fp8 MFMA, flop/s
-MALL_BYTES = 256 << 20       # Infinity Cache: timed buffers rotate over more than this
+import reng_ceiling as RC     # noqa: E402  (the package directory is on sys.path above)
+
+MI355X = RC.HardwareSpec.mi355x()
+HBM_PEAK = MI355X.hbm_bw     # 8 TB/s HBM3E, bytes/s
+MALL_BYTES = MI355X.sram_bytes   # Infinity Cache: timed buffers rotate over more than this
 
 LLAMA_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
             ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
@@ -49,8 +51,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def quant_bytes(rows, cols, in_bytes=2):
-    return rows * cols * (in_bytes + 1) + 4 * rows
+quant_bytes = RC.quantize_bytes
 
 
 def make_bf16(torch, rows, cols, gen, inject=True):
@@ -230,11 +231,12 @@ def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3"):
     y = torch.empty(M * N, dtype=torch.bfloat16, device="cuda")
     secs = graph_time(torch, lambda i: R.gemm_w8a16(x, ws[i % copies][0], ws[i % copies][1], M, N, K, fmt, y),
                       max(2 * copies, 40))
-    nbytes = N * K + 4 * N + 2 * M * K + 2 * M * N
+    nbytes = RC.w8a16_bytes(M, N, K)
     flops = 2 * M * N * K
+    ceil = RC.w8a16_ceiling(MI355X, M, N, K)   # HBM-bound for M <= 64
     return {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
-            "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "TFLOPs": round(flops / secs / 1e12, 2),
-            "rotated_copies": copies}
+            "hbm_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value,
+            "TFLOPs": round(flops / secs / 1e12, 2), "rotated_copies": copies}
 
 
 def bench_fp8_gemm(torch, R, gen, M, N, K):
@@ -247,8 +249,9 @@ def bench_fp8_gemm(torch, R, gen, M, N, K):
     secs = graph_time(torch, lambda i: R.gemm_fp8_scaled(qa.codes, "e4m3", qa.scales, qw.codes, "e4m3",
                                                          qw.scales, M, N, K, out), 10)
     flops = 2 * M * N * K
+    ceil = RC.fp8_gemm_ceiling(MI355X, M, N, K)   # fp8 MFMA-bound at M = 1024
     return {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 1), "TFLOPs": round(flops / secs / 1e12, 1),
-            "mfma_frac": round(flops / secs / FP8_PEAK, 3)}
+            "mfma_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value}
 
 
 def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048):
