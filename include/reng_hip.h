@@ -142,8 +142,9 @@ RENG_HIP_API int reng_hip_row_errors(const uint16_t *w, const uint8_t *codes, co
  * Quantized::dequantize (crates/reng-model/src/bin/fp8_probe.rs:55-67).
  * Shapes are row-major: x [M, K], codes [N, K], y [M, N] (the reference's
  * device sizes A [K, m], W [K, N] with transpose_b, out [N, m]).
- * Batches 1..64 use in-register fp8 decode (a GEMV for M = 1, and for M <= 4
- * when K is not a multiple of 128; bf16 MFMA otherwise); any M is accepted.
+ * Batches 1..64 use in-register fp8 decode (a GEMV for M = 1, M = 2 with
+ * K <= 16384, and M <= 4 when K is not a multiple of 128; bf16 MFMA
+ * otherwise); any M is accepted.
  * scales may be NULL (unit scale, the 2-input form).
  * Codes are the quantizer's finite codes; codes of the reserved top exponent
  * field are read as OCP values, not as +-inf/NaN. K must be a multiple of 16. */
