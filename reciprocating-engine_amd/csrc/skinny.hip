@@ -1,5 +1,6 @@
 // skinny.hip - y[m, n] = bf16(s[n] * sum_k x[m, k] * decode(c[n, k])) for
-// 4 < M <= 64 activation rows (bf16) on bf16 MFMA (gfx950).
+// up to 64 activation rows (bf16) on bf16 MFMA (gfx950); gemm.hip sends a
+// product of one row (or two with a short K) to its GEMV instead.
 //
 // The reference semantics are gemm_cpu over Quantized::dequantize
 // (crates/reng-model/src/bin/fp8_probe.rs:55-67) with the per-channel scaleB
@@ -110,6 +111,9 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
     constexpr int CA = AR ? 0 : MA / 2, C = 4 * NT + CA;   // copies per stage
     constexpr int ACT_BYTES = ACTK * MA * CHUNK * 2;       // [chunk][MA rows][256 B]
     static_assert(S >= 2 && (S - 1) * C < 64, "pipeline depth");
+    // Every wave must reach the barrier after the activation copies: with one
+    // run of K per wave (KW = 1) each wave has at least one chunk.
+    static_assert(!AR || KW == 1, "the resident activation needs KW = 1");
     constexpr int W = KW * NW;
     constexpr int RED = KW > 1 ? W * NT * 1024 : 0;
     constexpr int LDS0 = W * RING > RED ? W * RING : RED;
