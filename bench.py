@@ -270,6 +270,20 @@ def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048):
             "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "rotated_copies": copies}
 
 
+def bench_decode_step(layers=4, positions=512):
+    """The fp8 decode step (reng_model::Fp8Decoder) on Llama-3.1-8B-shaped layers:
+    bin/reng-fp8-decode-bench in a child process (its own HIP runtime, its own
+    device memory); its JSON line, or an error record if it fails."""
+    import subprocess
+
+    exe = os.path.join(ROOT, "reciprocating-engine_amd", "bin", "reng-fp8-decode-bench")
+    r = subprocess.run([exe, "--layers", str(layers), "--positions", str(positions)], capture_output=True,
+                       text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": (r.stderr or r.stdout).strip()[-500:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def read_traffic(kind):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC
     summary (profiles/<kind>_traffic.txt: `fetch_bytes` and `write_bytes` lines,
@@ -295,7 +309,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--extended", action="store_true", help="also the full Qwen2.5-32B quantize")
-    ap.add_argument("--part", default="all", choices=["all", "quantize", "gemv", "skinny", "prefill", "f32"],
+    ap.add_argument("--part", default="all",
+                    choices=["all", "quantize", "gemv", "skinny", "prefill", "f32", "decode"],
                     help="run one part only (for profiling); the JSON line is printed for 'all' and 'quantize'")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy 1 GiB device-to-device three times first: a kernel of known traffic that "
@@ -332,6 +347,8 @@ def main():
         elif args.part == "prefill":
             out = [bench_fp8_gemm(torch, R, gen, 1024, N, K) for N, K in ((5120, 5120), (1024, 5120),
                                                                            (27648, 5120), (5120, 27648))]
+        elif args.part == "decode":
+            out = [bench_decode_step()]
         else:
             out = [bench_f32_quantize(torch, R, gen)]
         log(json.dumps(out))
@@ -388,6 +405,8 @@ def main():
                                                             (5120, 27648))]
         log("prefill fp8:", extras["prefill_fp8_m1024_qwen32b"])
         torch.cuda.empty_cache()
+        extras["decode_step_llama8b"] = bench_decode_step()
+        log("decode step:", extras["decode_step_llama8b"])
         if args.extended:
             wq = WeightSet(torch, QWEN_32B, 64, seed=4321)
             r3 = time_quantize(torch, R, wq, "e4m3", 3, 1)

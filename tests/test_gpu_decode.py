@@ -153,6 +153,46 @@ def test_decode_from_saved_codes_equals_the_fresh_quantize(tmp_path):
     assert r.returncode == 1 and "no current model.fp8.safetensors" in r.stderr
 
 
+DECODE_BENCH = os.path.join(ROOT, "reciprocating-engine_amd", "bin", "reng-fp8-decode-bench")
+
+
+def _decode_bench(*args, timeout=60):
+    if not os.path.exists(DECODE_BENCH):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "reciprocating-engine_amd")], check=True,
+                       capture_output=True)
+    return subprocess.run([DECODE_BENCH, *args], capture_output=True, text=True, timeout=timeout)
+
+
+def test_decode_bench_refuses_bad_flags():
+    """Refused before any device work."""
+    r = _decode_bench("--layers", "0")
+    assert r.returncode == 1 and "--layers: not a positive integer: 0" in r.stderr
+    r = _decode_bench("--hidden", "100", "--heads", "8")
+    assert r.returncode == 1 and "hidden must divide into heads" in r.stderr
+    r = _decode_bench("--positions")
+    assert r.returncode == 1 and "--positions needs a value" in r.stderr
+    r = _decode_bench("--bogus", "1")
+    assert r.returncode == 1 and "unknown flag --bogus" in r.stderr
+
+
+@pytest.mark.gpu
+def test_decode_bench_times_a_small_stack():
+    r = _decode_bench("--layers", "2", "--positions", "24", "--hidden", "256", "--intermediate", "512",
+                      "--heads", "8", "--kv-heads", "2", timeout=110)
+    assert r.returncode == 0, r.stdout + r.stderr
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    assert d["output_finite"] is True and d["us_per_layer_step"] > 0
+    assert (d["layers"], d["positions"], d["head_dim"]) == (2, 24, 32)
+    # codes + scales of one layer: q, k, v, o [256|64, 256], gate, up [512, 256], down [256, 512]
+    codes = 256 * 256 * 2 + 64 * 256 * 2 + 512 * 256 * 3
+    scales = 4 * (256 + 64 + 64 + 256 + 512 + 512 + 256)
+    assert d["bytes_per_layer_step"] == pytest.approx(codes + scales + 2 * 12.5 * 64 * 2)
+    # Past max_positions the step is refused.
+    r = _decode_bench("--positions", "15001", "--layers", "1", "--hidden", "256", "--intermediate", "512",
+                      "--heads", "8", "--kv-heads", "2", timeout=110)
+    assert r.returncode == 1 and "max_positions 15001" in r.stderr
+
+
 def test_decode_step_entry_points_refuse_bad_arguments():
     """Refused before any device work (EINVAL), so no GPU is needed."""
     import ctypes
