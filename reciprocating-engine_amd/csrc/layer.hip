@@ -5,7 +5,7 @@
 //   q, k, v = n W{q,k,v}^T                           (fp8 GEMV)
 //   rotate-half RoPE of q and k at position p; k, v
 //   appended to the layer's bf16 cache as row p      reng_hip_rope_append
-//   a  = softmax(scale q K^T) V over rows 0..p       reng_hip_attention_decode
+//   a  = softmax(scale q K^T) V over rows 0..p       reng_hip_attention_decode(_split)
 //   h  = x + a Wo^T                                  (fp8 GEMV) + reng_hip_add_bf16_f32
 //   n2 = bf16(rms_norm(h, g2)); g, u = n2 W{g,u}^T   reng_hip_rms_norm_bf16, (fp8 GEMV)
 //   y  = h + (silu(g) * u) Wd^T                      reng_hip_silu_mul_bf16, (fp8 GEMV), add
@@ -97,46 +97,251 @@ __global__ __launch_bounds__(64) void rope_append(uint16_t *__restrict__ q, cons
     }
 }
 
-// One query per head over cache rows 0 .. len - 1 (the causal row of
+// ---------------------------------------------------------------- attention
+//
+// One query row per head against cache rows 0 .. len - 1 (the causal row of
 // layer_cpu's attention, model.rs:3010-3050): s_j = scale * q_h . k_j[g],
-// p = softmax(s), out_h = sum_j p_j v_j[g], with g = h / (nh / nkv). One
-// block per head; the scores live in LDS (len floats) and q in f32.
-__global__ __launch_bounds__(256) void attention_decode(const uint16_t *__restrict__ q,
-                                                        const uint16_t *__restrict__ kc,
-                                                        const uint16_t *__restrict__ vc, uint32_t nh,
-                                                        uint32_t nkv, uint32_t hd, uint32_t len, float scale,
-                                                        uint16_t *__restrict__ out) {
-    extern __shared__ float smem[];
-    float *qs = smem;            // hd
-    float *s = smem + hd;        // len
-    __shared__ float red[4];
-    const uint32_t h = blockIdx.x, g = h / (nh / nkv), pitch = nkv * hd;
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = bf16_f32(q[(size_t)h * hd + d]);
+// p = softmax(s), out_h = sum_j p_j v_j[g], with g = h / (nh / nkv).
+//
+// The cache is cut into S splits of `chunk` rows; workgroup (s, y) reads the
+// key and value rows of split s once for a group of gb query heads that share
+// key/value head g (gb divides nh / nkv, at most ATT_GMAX), 64 rows at a time
+// with an online softmax: per tile, phase 1 puts the tile's scores in LDS
+// (16 lanes per key row, 16-byte loads when head_dim % 8 == 0), the tile's
+// max and sum update the running (m, l) per head, and phase 2 accumulates
+// exp(s_j - m) v_j into registers (a thread per value-row dimension pair and
+// row phase, so each wave load is whole rows). With S = 1 the workgroup
+// writes bf16(o / l); otherwise it writes the unnormalised o and (m, l) of its
+// split to the workspace and attention_combine merges the splits.
+constexpr int ATT_THREADS = 256, ATT_TILE = 64, ATT_GMAX = 8, ATT_SPLIT_MAX = 64, ATT_SPLIT_ROWS = 32;
+
+struct AttnPlan {
+    uint32_t splits, chunk;
+};
+
+// S = min(64, ceil(len / 32)) splits of equal length (the last one shorter),
+// none empty.
+inline AttnPlan attn_plan(size_t len, bool split) {
+    if (!split) return {1u, (uint32_t)len};
+    size_t s = (len + ATT_SPLIT_ROWS - 1) / ATT_SPLIT_ROWS;
+    if (s > (size_t)ATT_SPLIT_MAX) s = ATT_SPLIT_MAX;
+    const size_t chunk = (len + s - 1) / s;
+    return {(uint32_t)((len + chunk - 1) / chunk), (uint32_t)chunk};
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum over each 16-lane row, left in the row's lane 15.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0x111, 0xf>(v);   // row_shr:1
+    v += dpp_mov<0x112, 0xf>(v);   // row_shr:2
+    v += dpp_mov<0x114, 0xf>(v);   // row_shr:4
+    v += dpp_mov<0x118, 0xf>(v);   // row_shr:8
+    return v;
+}
+
+template <bool V8>
+__global__ __launch_bounds__(ATT_THREADS) void attention_split(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, uint32_t nh,
+    uint32_t nkv, uint32_t hd, uint32_t len, uint32_t chunk, uint32_t gb, float scale, float *__restrict__ part,
+    uint16_t *__restrict__ out) {
+    extern __shared__ float smem[];   // q [gb][hd] f32; after the tiles, o [nph][gb][hd]
+    __shared__ float sc[ATT_GMAX][ATT_TILE];
+    __shared__ float mrun[ATT_GMAX], lrun[ATT_GMAX], corr[ATT_GMAX];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t s = blockIdx.x, h0 = blockIdx.y * gb, g = h0 / (nh / nkv);
+    const size_t pitch = (size_t)nkv * hd;
+    const uint32_t j0 = s * chunk, j1 = min(len, j0 + chunk);
+    const uint16_t *kbase = kc + (size_t)g * hd, *vbase = vc + (size_t)g * hd;
+    float *qs = smem;
+    for (uint32_t i = tid; i < gb * hd; i += ATT_THREADS) qs[i] = bf16_f32(q[(size_t)h0 * hd + i]);
+    if (tid < ATT_GMAX) {
+        mrun[tid] = -INFINITY;
+        lrun[tid] = 0.0f;
+    }
+    // Phase 2 mapping: dimension pair dp (and dp + 256 when head_dim > 512) of
+    // the rows ph, ph + nph, ... of a tile.
+    const uint32_t npairs = hd / 2, dpb = npairs < ATT_THREADS ? npairs : ATT_THREADS, nph = ATT_THREADS / dpb;
+    const uint32_t ph = tid / dpb, dp = tid % dpb;
+    const bool active = ph < nph;
+    float o[ATT_GMAX][2][2];
+#pragma unroll
+    for (int h = 0; h < ATT_GMAX; ++h)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) o[h][e][0] = o[h][e][1] = 0.0f;
     __syncthreads();
-    float mx = -INFINITY;
-    for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
-        const uint16_t *kr = kc + (size_t)j * pitch + (size_t)g * hd;
-        float acc = 0.0f;
-        for (uint32_t d = 0; d < hd; d += 2) {
-            const uint32_t w = *reinterpret_cast<const uint32_t *>(kr + d);
-            acc += qs[d] * __uint_as_float(w << 16) + qs[d + 1] * __uint_as_float(w & 0xffff0000u);
+
+    const uint32_t l16 = lane & 15, rg = lane >> 4;
+    for (uint32_t t0 = j0; t0 < j1; t0 += ATT_TILE) {
+        const uint32_t n = min((uint32_t)ATT_TILE, j1 - t0);
+        // Phase 1: rows wave * 16 + it * 4 + rg of the tile.
+        float acc[4][ATT_GMAX];
+#pragma unroll
+        for (int it = 0; it < 4; ++it)
+#pragma unroll
+            for (int h = 0; h < ATT_GMAX; ++h) acc[it][h] = 0.0f;
+        if constexpr (V8) {
+            const uint32_t npc = hd / 8;
+            for (uint32_t pc = l16; pc < npc; pc += 16) {
+                uint4 kv[4];
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const uint32_t jj = wave * 16 + it * 4 + rg;
+                    kv[it] = jj < n ? *reinterpret_cast<const uint4 *>(kbase + (size_t)(t0 + jj) * pitch + 8 * pc)
+                                    : uint4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int h = 0; h < ATT_GMAX; ++h) {
+                    if (h >= (int)gb) break;
+                    const float4 qa = *reinterpret_cast<const float4 *>(qs + h * hd + 8 * pc);
+                    const float4 qb = *reinterpret_cast<const float4 *>(qs + h * hd + 8 * pc + 4);
+#pragma unroll
+                    for (int it = 0; it < 4; ++it) {
+                        const uint4 w = kv[it];
+                        float a = acc[it][h];
+                        a += qa.x * __uint_as_float(w.x << 16) + qa.y * __uint_as_float(w.x & 0xffff0000u);
+                        a += qa.z * __uint_as_float(w.y << 16) + qa.w * __uint_as_float(w.y & 0xffff0000u);
+                        a += qb.x * __uint_as_float(w.z << 16) + qb.y * __uint_as_float(w.z & 0xffff0000u);
+                        a += qb.z * __uint_as_float(w.w << 16) + qb.w * __uint_as_float(w.w & 0xffff0000u);
+                        acc[it][h] = a;
+                    }
+                }
+            }
+        } else {
+            const uint32_t npc = hd / 2;
+            for (uint32_t pc = l16; pc < npc; pc += 16) {
+                uint32_t kv[4];
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const uint32_t jj = wave * 16 + it * 4 + rg;
+                    kv[it] = jj < n ? *reinterpret_cast<const uint32_t *>(kbase + (size_t)(t0 + jj) * pitch + 2 * pc)
+                                    : 0u;
+                }
+#pragma unroll
+                for (int h = 0; h < ATT_GMAX; ++h) {
+                    if (h >= (int)gb) break;
+                    const float2 qa = *reinterpret_cast<const float2 *>(qs + h * hd + 2 * pc);
+#pragma unroll
+                    for (int it = 0; it < 4; ++it)
+                        acc[it][h] += qa.x * __uint_as_float(kv[it] << 16) + qa.y * __uint_as_float(kv[it] & 0xffff0000u);
+                }
+            }
         }
-        s[j] = acc * scale;
-        mx = fmaxf(mx, s[j]);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const uint32_t jj = wave * 16 + it * 4 + rg;
+#pragma unroll
+            for (int h = 0; h < ATT_GMAX; ++h) {
+                if (h >= (int)gb) break;
+                const float v = row16_sum(acc[it][h]);
+                if (l16 == 15) sc[h][jj] = jj < n ? v * scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // Running max and sum: wave w owns heads w and w + 4.
+        for (uint32_t h = wave; h < gb; h += 4) {
+            const float v = sc[h][lane];
+            const float mo = mrun[h], mn = fmaxf(mo, wave_max_f32(v));
+            const float p = lane < n ? expf(v - mn) : 0.0f;
+            const float ps = wave_sum_dpp(p);
+            sc[h][lane] = p;
+            if (lane == 0) {
+                const float c = expf(mo - mn);   // 0 on the first tile (mo = -inf)
+                corr[h] = c;
+                lrun[h] = lrun[h] * c + ps;
+                mrun[h] = mn;
+            }
+        }
+        __syncthreads();
+        // Phase 2.
+        if (active) {
+#pragma unroll
+            for (int h = 0; h < ATT_GMAX; ++h) {
+                if (h >= (int)gb) break;
+                const float c = corr[h];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    o[h][e][0] *= c;
+                    o[h][e][1] *= c;
+                }
+            }
+            const bool two = dp + ATT_THREADS < npairs;
+            for (uint32_t jj = ph; jj < n; jj += nph) {
+                const uint16_t *vr = vbase + (size_t)(t0 + jj) * pitch;
+                const uint32_t w0 = *reinterpret_cast<const uint32_t *>(vr + 2 * dp);
+                const uint32_t w1 = two ? *reinterpret_cast<const uint32_t *>(vr + 2 * (dp + ATT_THREADS)) : 0u;
+                const float a0 = __uint_as_float(w0 << 16), a1 = __uint_as_float(w0 & 0xffff0000u);
+                const float b0 = __uint_as_float(w1 << 16), b1 = __uint_as_float(w1 & 0xffff0000u);
+#pragma unroll
+                for (int h = 0; h < ATT_GMAX; ++h) {
+                    if (h >= (int)gb) break;
+                    const float p = sc[h][jj];
+                    o[h][0][0] += p * a0;
+                    o[h][0][1] += p * a1;
+                    o[h][1][0] += p * b0;
+                    o[h][1][1] += p * b1;
+                }
+            }
+        }
+        __syncthreads();
     }
-    mx = block_max(mx, red);
-    float sum = 0.0f;
-    for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
-        const float e = expf(s[j] - mx);
-        s[j] = e;
-        sum += e;
+    // Sum the row phases' o in LDS (the q copy is no longer read).
+    float *op = smem;   // [nph][gb][hd]
+    if (active) {
+#pragma unroll
+        for (int h = 0; h < ATT_GMAX; ++h) {
+            if (h >= (int)gb) break;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t d = 2 * (dp + e * ATT_THREADS);
+                if (d < hd) {
+                    op[((size_t)ph * gb + h) * hd + d] = o[h][e][0];
+                    op[((size_t)ph * gb + h) * hd + d + 1] = o[h][e][1];
+                }
+            }
+        }
     }
-    sum = block_sum(sum, red);   // its barriers also publish s[]
-    const float inv = 1.0f / sum;
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-        float acc = 0.0f;
-        for (uint32_t j = 0; j < len; ++j) acc += s[j] * bf16_f32(vc[(size_t)j * pitch + (size_t)g * hd + d]);
-        out[(size_t)h * hd + d] = f32_bf16(acc * inv);
+    __syncthreads();
+    for (uint32_t i = tid; i < gb * hd; i += ATT_THREADS) {
+        const uint32_t h = i / hd;
+        float v = 0.0f;
+        for (uint32_t r = 0; r < nph; ++r) v += op[(size_t)r * gb * hd + i];
+        if (part == nullptr) {
+            out[(size_t)h0 * hd + i] = f32_bf16(v / lrun[h]);
+        } else {
+            part[((size_t)s * nh + h0) * hd + i] = v;
+        }
+    }
+    if (part != nullptr && tid < gb) {
+        float *ml = part + (size_t)gridDim.x * nh * hd;
+        ml[((size_t)s * nh + h0 + tid) * 2] = mrun[tid];
+        ml[((size_t)s * nh + h0 + tid) * 2 + 1] = lrun[tid];
+    }
+}
+
+// out_h = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s): the
+// splits of attention_split merged. One workgroup per head.
+__global__ __launch_bounds__(ATT_THREADS) void attention_combine(const float *__restrict__ part, uint32_t nh,
+                                                                 uint32_t hd, uint32_t splits,
+                                                                 uint16_t *__restrict__ out) {
+    __shared__ float wsp[ATT_SPLIT_MAX];
+    __shared__ float red[4];
+    const uint32_t h = blockIdx.x, tid = threadIdx.x;
+    const float *ml = part + (size_t)splits * nh * hd;
+    const float m = tid < splits ? ml[((size_t)tid * nh + h) * 2] : -INFINITY;
+    const float mx = block_max(m, red);
+    const float w = tid < splits ? expf(m - mx) : 0.0f;
+    const float den = block_sum(tid < splits ? w * ml[((size_t)tid * nh + h) * 2 + 1] : 0.0f, red);
+    if (tid < splits) wsp[tid] = w / den;
+    __syncthreads();
+    for (uint32_t d = tid; d < hd; d += ATT_THREADS) {
+        float v = 0.0f;
+        for (uint32_t i = 0; i < splits; ++i) v += wsp[i] * part[((size_t)i * nh + h) * hd + d];
+        out[(size_t)h * hd + d] = f32_bf16(v);
     }
 }
 
@@ -201,10 +406,22 @@ RENG_HIP_API int reng_hip_rope_append(uint16_t *q, const uint16_t *k, const uint
     return check_launch("rope_append");
 }
 
-RENG_HIP_API int reng_hip_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
-                                           size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t len,
-                                           float scale, uint16_t *out, void *stream) {
-    clear_error();
+namespace {
+
+// The largest divisor of the query heads per key/value head that is at most
+// ATT_GMAX: the heads one workgroup serves from one read of the cache.
+uint32_t head_group(size_t per_kv) {
+    for (size_t g = per_kv < (size_t)ATT_GMAX ? per_kv : (size_t)ATT_GMAX; g > 1; --g)
+        if (per_kv % g == 0) return (uint32_t)g;
+    return 1;
+}
+
+size_t split_part_bytes(size_t splits, size_t n_heads, size_t head_dim) {
+    return splits < 2 ? 0 : splits * n_heads * (head_dim + 2) * sizeof(float);
+}
+
+int attention_args(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache, size_t n_heads,
+                   size_t n_kv_heads, size_t head_dim, size_t len, const uint16_t *out) {
     RENG_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
                  "%zu query heads are not a multiple of %zu key/value heads", n_heads, n_kv_heads);
     RENG_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 1024, "head_dim %zu is not even in [2, 1024]",
@@ -213,12 +430,66 @@ RENG_HIP_API int reng_hip_attention_decode(const uint16_t *q, const uint16_t *k_
                  RENG_HIP_ATTENTION_MAX_LEN);
     RENG_REQUIRE(n_heads <= 0x7fffffff, "too many heads");
     RENG_REQUIRE(q && k_cache && v_cache && out, "null pointer");
-    RENG_REQUIRE((reinterpret_cast<uintptr_t>(k_cache) & 3) == 0, "k_cache must be 4-byte aligned");
-    const size_t lds = (head_dim + len) * sizeof(float);
-    hipLaunchKernelGGL(attention_decode, dim3((unsigned)n_heads), dim3(256), lds, stream_of(stream), q, k_cache,
-                       v_cache, (uint32_t)n_heads, (uint32_t)n_kv_heads, (uint32_t)head_dim, (uint32_t)len, scale,
-                       out);
-    return check_launch("attention_decode");
+    RENG_REQUIRE((reinterpret_cast<uintptr_t>(k_cache) & 3) == 0 && (reinterpret_cast<uintptr_t>(v_cache) & 3) == 0,
+                 "k_cache and v_cache must be 4-byte aligned");
+    return RENG_HIP_OK;
+}
+
+int launch_attention(const uint16_t *q, const uint16_t *kc, const uint16_t *vc, size_t nh, size_t nkv, size_t hd,
+                     size_t len, float scale, float *part, uint16_t *out, hipStream_t st) {
+    const AttnPlan p = attn_plan(len, part != nullptr);
+    const uint32_t gb = p.splits > 1 ? head_group(nh / nkv) : 1u;
+    const size_t npairs = hd / 2, dpb = npairs < (size_t)ATT_THREADS ? npairs : (size_t)ATT_THREADS;
+    const size_t lds = (ATT_THREADS / dpb) * gb * hd * sizeof(float);
+    const bool v8 = hd % 8 == 0 && (reinterpret_cast<uintptr_t>(kc) & 15) == 0;
+    float *wp = p.splits > 1 ? part : nullptr;
+    const dim3 grid(p.splits, (unsigned)(nh / gb));
+    if (v8)
+        hipLaunchKernelGGL(attention_split<true>, grid, dim3(ATT_THREADS), lds, st, q, kc, vc, (uint32_t)nh,
+                           (uint32_t)nkv, (uint32_t)hd, (uint32_t)len, p.chunk, gb, scale, wp, out);
+    else
+        hipLaunchKernelGGL(attention_split<false>, grid, dim3(ATT_THREADS), lds, st, q, kc, vc, (uint32_t)nh,
+                           (uint32_t)nkv, (uint32_t)hd, (uint32_t)len, p.chunk, gb, scale, wp, out);
+    if (int rc = check_launch("attention_split")) return rc;
+    if (p.splits < 2) return RENG_HIP_OK;
+    hipLaunchKernelGGL(attention_combine, dim3((unsigned)nh), dim3(ATT_THREADS), 0, st, wp, (uint32_t)nh,
+                       (uint32_t)hd, p.splits, out);
+    return check_launch("attention_combine");
+}
+
+}  // namespace
+
+RENG_HIP_API int reng_hip_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                                           size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t len,
+                                           float scale, uint16_t *out, void *stream) {
+    clear_error();
+    if (int rc = attention_args(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, len, out)) return rc;
+    return launch_attention(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, len, scale, nullptr, out,
+                            stream_of(stream));
+}
+
+RENG_HIP_API size_t reng_hip_attention_workspace_bytes(size_t n_heads, size_t head_dim, size_t len) {
+    if (len > RENG_HIP_ATTENTION_MAX_LEN) len = RENG_HIP_ATTENTION_MAX_LEN;
+    size_t s = (len + ATT_SPLIT_ROWS - 1) / ATT_SPLIT_ROWS;
+    if (s > (size_t)ATT_SPLIT_MAX) s = ATT_SPLIT_MAX;
+    if (n_heads > 0x7fffffff || head_dim > 1024) return 0;
+    return split_part_bytes(s, n_heads, head_dim);
+}
+
+RENG_HIP_API int reng_hip_attention_decode_split(const uint16_t *q, const uint16_t *k_cache,
+                                                 const uint16_t *v_cache, size_t n_heads, size_t n_kv_heads,
+                                                 size_t head_dim, size_t len, float scale, void *workspace,
+                                                 size_t workspace_bytes, uint16_t *out, void *stream) {
+    clear_error();
+    if (int rc = attention_args(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, len, out)) return rc;
+    const size_t need = split_part_bytes(attn_plan(len, true).splits, n_heads, head_dim);
+    RENG_REQUIRE(workspace_bytes >= need, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    RENG_REQUIRE(need == 0 || workspace, "null workspace");
+    RENG_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 3) == 0, "workspace must be 4-byte aligned");
+    // A cache short enough for one split takes the one-pass form and leaves the workspace alone.
+    float *part = need ? static_cast<float *>(workspace) : nullptr;
+    return launch_attention(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, len, scale, part, out,
+                            stream_of(stream));
 }
 
 RENG_HIP_API int reng_hip_silu_mul_bf16(const uint16_t *gate, const uint16_t *up, size_t n, uint16_t *out,

@@ -174,7 +174,7 @@ int run(int argc, char **argv) {
     std::printf("{\"workload\": \"fp8 decode step, Llama-shaped layer\", \"hidden\": %zu, \"intermediate\": %zu, "
                 "\"heads\": %zu, \"kv_heads\": %zu, \"head_dim\": %zu, \"layers\": %zu, \"positions\": %zu, "
                 "\"us_per_layer_step\": %.2f, \"tokens_per_s_per_layer\": %.0f, \"bytes_per_layer_step\": %.0f, "
-                "\"GBps\": %.1f, \"hbm_frac\": %.3f, \"kernels_per_layer_step\": 12, \"host_wall_s\": %.3f, "
+                "\"GBps\": %.1f, \"hbm_frac\": %.3f, \"host_wall_s\": %.3f, "
                 "\"output_finite\": %s}\n",
                 a.hidden, a.inter, a.heads, a.kv, hd, a.layers, a.positions, us, 1e6 / us, bytes,
                 bytes / (us * 1e-6) / 1e9, bytes / (us * 1e-6) / 8.0e12, wall, finite ? "true" : "false");

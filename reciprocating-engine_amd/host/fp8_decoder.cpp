@@ -120,6 +120,8 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
         up_ = static_cast<uint16_t *>(dev(inter_ * 2));
         act_ = static_cast<uint16_t *>(dev(inter_ * 2));
         down_ = static_cast<uint16_t *>(dev(hidden_ * 2));
+        attn_ws_bytes_ = reng_hip_attention_workspace_bytes(nh_, hd_, max_pos_);
+        attn_ws_ = dev(attn_ws_bytes_);
     } catch (...) {
         for (void *p : allocs_) (void)hipFree(p);
         allocs_.clear();
@@ -149,7 +151,8 @@ void Fp8Decoder::step_device(size_t li, const float *x, float *y, size_t pos, vo
     gemv(L.wv, n_, v_, stream);
     abi_ok(reng_hip_rope_append(q_, k_, v_, nh_, nkv_, hd_, sin_ + pos * hd_, cos_ + pos * hd_,
                                 L.kcache + pos * kvd, L.vcache + pos * kvd, stream));
-    abi_ok(reng_hip_attention_decode(q_, L.kcache, L.vcache, nh_, nkv_, hd_, pos + 1, scale_, a_, stream));
+    abi_ok(reng_hip_attention_decode_split(q_, L.kcache, L.vcache, nh_, nkv_, hd_, pos + 1, scale_, attn_ws_,
+                                           attn_ws_bytes_, a_, stream));
     gemv(L.wo, a_, o_, stream);
     abi_ok(reng_hip_add_bf16_f32(x, o_, hidden_, h_, stream));
     abi_ok(reng_hip_rms_norm_bf16(h_, L.g2, 1, hidden_, eps_, n_, stream));

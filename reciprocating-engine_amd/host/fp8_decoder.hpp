@@ -75,6 +75,9 @@ class Fp8Decoder {
     float *x_ = nullptr, *h_ = nullptr;
     uint16_t *n_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *a_ = nullptr, *o_ = nullptr;
     uint16_t *gate_ = nullptr, *up_ = nullptr, *act_ = nullptr, *down_ = nullptr;
+    // the split attention's partial outputs (one layer at a time)
+    void *attn_ws_ = nullptr;
+    size_t attn_ws_bytes_ = 0;
 };
 
 }  // namespace reng_model

@@ -62,6 +62,8 @@ SIGNATURES = {
     "reng_hip_rms_norm_bf16": (_I, [_P, _P, _SZ, _SZ, _F, _P, _P]),
     "reng_hip_rope_append": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P]),
     "reng_hip_attention_decode": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _P]),
+    "reng_hip_attention_workspace_bytes": (_SZ, [_SZ, _SZ, _SZ]),
+    "reng_hip_attention_decode_split": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _SZ, _P, _P]),
     "reng_hip_silu_mul_bf16": (_I, [_P, _P, _SZ, _P, _P]),
     "reng_hip_add_bf16_f32": (_I, [_P, _P, _SZ, _P, _P]),
 }
@@ -343,6 +345,31 @@ def attention_decode(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, length,
         out = torch.empty(n_heads * head_dim, dtype=torch.bfloat16, device=q.device)
     _check(lib().reng_hip_attention_decode(_dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), n_heads,
                                            n_kv_heads, head_dim, length, scale, _dev(out, "out"), _stream()))
+    return out
+
+
+def attention_workspace_bytes(n_heads, head_dim, length):
+    """Device workspace attention_decode_split needs for caches of 1 .. length rows."""
+    return lib().reng_hip_attention_workspace_bytes(n_heads, head_dim, length)
+
+
+def attention_decode_split(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, length, scale, workspace=None,
+                           out=None):
+    """attention_decode with the cache split over workgroups and merged; workspace
+    a device tensor of at least attention_workspace_bytes(...) bytes (allocated
+    here when None)."""
+    import torch
+
+    if out is None:
+        out = torch.empty(n_heads * head_dim, dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        workspace = torch.empty(max(1, attention_workspace_bytes(n_heads, head_dim, length)), dtype=torch.uint8,
+                                device=q.device)
+    _check(lib().reng_hip_attention_decode_split(_dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"),
+                                                 n_heads, n_kv_heads, head_dim, length, scale,
+                                                 _dev(workspace, "workspace"),
+                                                 workspace.numel() * workspace.element_size(), _dev(out, "out"),
+                                                 _stream()))
     return out
 
 

@@ -188,9 +188,9 @@ def test_decode_bench_times_a_small_stack():
     scales = 4 * (256 + 64 + 64 + 256 + 512 + 512 + 256)
     assert d["bytes_per_layer_step"] == pytest.approx(codes + scales + 2 * 12.5 * 64 * 2)
     # Past max_positions the step is refused.
-    r = _decode_bench("--positions", "15001", "--layers", "1", "--hidden", "256", "--intermediate", "512",
+    r = _decode_bench("--positions", "131073", "--layers", "1", "--hidden", "256", "--intermediate", "512",
                       "--heads", "8", "--kv-heads", "2", timeout=110)
-    assert r.returncode == 1 and "max_positions 15001" in r.stderr
+    assert r.returncode == 1 and "max_positions 131073" in r.stderr
 
 
 def test_decode_step_entry_points_refuse_bad_arguments():
@@ -207,10 +207,22 @@ def test_decode_step_entry_points_refuse_bad_arguments():
     assert lib.reng_hip_rope_append(p, p, p, 6, 4, 64, p, p, p, p, None) == R.EINVAL       # 6 % 4
     assert lib.reng_hip_rope_append(p, p, p, 4, 2, 63, p, p, p, p, None) == R.EINVAL       # odd head_dim
     assert lib.reng_hip_attention_decode(p, p, p, 4, 2, 64, 0, 1.0, p, None) == R.EINVAL   # empty cache
-    assert lib.reng_hip_attention_decode(p, p, p, 4, 2, 64, 15001, 1.0, p, None) == R.EINVAL
+    assert lib.reng_hip_attention_decode(p, p, p, 4, 2, 64, 131073, 1.0, p, None) == R.EINVAL
     assert b"cache length" in lib.reng_hip_last_error()
     assert lib.reng_hip_attention_decode(ctypes.c_void_p(18), ctypes.c_void_p(18), p, 4, 2, 64, 3, 1.0, p,
                                          None) == R.EINVAL                                # misaligned k_cache
+    assert lib.reng_hip_attention_decode(p, p, ctypes.c_void_p(18), 4, 2, 64, 3, 1.0, p,
+                                         None) == R.EINVAL                                # misaligned v_cache
+    # The split form: its workspace covers every length up to the one asked for.
+    need = lib.reng_hip_attention_workspace_bytes(4, 64, 700)
+    assert need == 22 * 4 * 66 * 4                      # ceil(700 / 32) = 22 splits of (o, m, l) per head
+    assert lib.reng_hip_attention_workspace_bytes(4, 64, 32) == 0
+    assert lib.reng_hip_attention_workspace_bytes(32, 128, 4096) == 64 * 32 * 130 * 4
+    assert lib.reng_hip_attention_workspace_bytes(32, 128, 10 ** 9) == 64 * 32 * 130 * 4
+    assert lib.reng_hip_attention_decode_split(p, p, p, 4, 2, 64, 700, 1.0, p, need - 4, p, None) == R.EINVAL
+    assert b"workspace of" in lib.reng_hip_last_error()
+    assert lib.reng_hip_attention_decode_split(p, p, p, 4, 2, 64, 700, 1.0, None, need, p, None) == R.EINVAL
+    assert lib.reng_hip_attention_decode_split(p, p, p, 4, 2, 64, 0, 1.0, p, need, p, None) == R.EINVAL
     assert lib.reng_hip_silu_mul_bf16(p, p, 0, p, None) == R.EINVAL
     assert lib.reng_hip_add_bf16_f32(p, None, 4, p, None) == R.EINVAL
 
@@ -272,3 +284,55 @@ def test_decode_step_kernels_against_numpy():
     xr = rng.standard_normal(999).astype(np.float32)
     out = R.add_bf16_f32(dev(xr), dev(up.view(np.int16)), 999).cpu().numpy()
     assert np.array_equal(out, xr + bf16_f32(up))
+
+
+def _attention_want(Q, K, V, nh, nkv, hd, scale):
+    want = np.zeros(nh * hd, dtype=np.float64)
+    for h in range(nh):
+        gi = h // (nh // nkv)
+        s = K[:, gi * hd:(gi + 1) * hd].astype(np.float64) @ Q[h * hd:(h + 1) * hd] * scale
+        e = np.exp(s - s.max())
+        want[h * hd:(h + 1) * hd] = (e / e.sum()) @ V[:, gi * hd:(gi + 1) * hd]
+    return want.astype(np.float32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nh,nkv,hd", [(6, 2, 64), (32, 8, 128), (4, 4, 6), (2, 1, 1024), (16, 1, 128)])
+def test_attention_forms_against_numpy(nh, nkv, hd):
+    """Both attention entry points against float64 numpy softmax attention:
+    lengths around the split threshold (32 rows) and the 64-row tile, long
+    caches that take 64 splits, head_dim not a multiple of 8 (the 4-byte
+    key path), head_dim 1024 (two value pairs per thread), one key/value head
+    for 16 query heads (head groups of 8), and a key cache 4 bytes off a
+    16-byte boundary (the 4-byte key path at head_dim % 8 == 0). The split
+    form's workspace starts as NaN, so a split it fails to write shows up."""
+    import torch
+
+    import reng_hip as R
+
+    rng = np.random.default_rng(nh * 1000 + hd)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    scale = hd ** -0.5
+    lengths = (1, 31, 32, 33, 64, 65, 700, 5000) if hd <= 128 else (1, 33, 700)
+    ws = torch.full((R.attention_workspace_bytes(nh, hd, max(lengths)) // 4 + 1,), float("nan"),
+                    dtype=torch.float32, device="cuda")
+    for length in lengths:
+        kb = bf16_bits(rng.standard_normal((length, nkv * hd)).astype(np.float32) * 2)
+        vb = bf16_bits(rng.standard_normal((length, nkv * hd)).astype(np.float32))
+        qb = bf16_bits(rng.standard_normal(nh * hd).astype(np.float32))
+        want = _attention_want(bf16_f32(qb), bf16_f32(kb), bf16_f32(vb), nh, nkv, hd, scale)
+        dq, dk, dv = dev(qb.view(np.int16)), dev(kb.view(np.int16).ravel()), dev(vb.view(np.int16).ravel())
+        one = bf16_f32(bits(R.attention_decode(dq, dk, dv, nh, nkv, hd, length, scale)))
+        split = bf16_f32(bits(R.attention_decode_split(dq, dk, dv, nh, nkv, hd, length, scale, workspace=ws)))
+        if length == 1:
+            assert np.array_equal(bf16_bits(one), bf16_bits(want)) and np.array_equal(bf16_bits(split),
+                                                                                    bf16_bits(want))
+        assert O.rel_l2(one, want) < 4e-3, (length, "one pass")
+        assert O.rel_l2(split, want) < 4e-3, (length, "split")
+        # the same key cache 4 bytes past a 16-byte boundary
+        if hd % 8 == 0 and length in (33, 700):
+            kk = torch.zeros(dk.numel() + 2, dtype=torch.int16, device="cuda")
+            kk[2:] = dk
+            off = bf16_f32(bits(R.attention_decode_split(dq, kk[2:], dv, nh, nkv, hd, length, scale, workspace=ws)))
+            assert O.rel_l2(off, want) < 4e-3, (length, "4-byte keys")
