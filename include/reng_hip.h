@@ -185,6 +185,12 @@ RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const 
 RENG_HIP_API int reng_hip_rms_norm_bf16(const float *x, const float *gamma, size_t rows, size_t cols, float eps,
                                         uint16_t *out, void *stream);
 
+/* h = x + d and out = bf16(rms_norm(h) * gamma) in one pass, x and h f32, d
+ * bf16 [rows, cols] (a branch output added to the residual stream, then the
+ * next sublayer's RMSNorm; h must not overlap x or d). */
+RENG_HIP_API int reng_hip_add_rms_norm_bf16(const float *x, const uint16_t *d, const float *gamma, size_t rows,
+                                            size_t cols, float eps, float *h, uint16_t *out, void *stream);
+
 /* Rotate-half RoPE of one position (rope_cpu, ops.rs:118-135) with the row
  * sin_row / cos_row [head_dim] of the tables: q [n_heads * head_dim] bf16 in
  * place; k [n_kv_heads * head_dim] rotated into k_row and v copied into v_row

@@ -6,8 +6,8 @@
 //   rotate-half RoPE of q and k at position p; k, v
 //   appended to the layer's bf16 cache as row p      reng_hip_rope_append
 //   a  = softmax(scale q K^T) V over rows 0..p       reng_hip_attention_decode(_split)
-//   h  = x + a Wo^T                                  (fp8 GEMV) + reng_hip_add_bf16_f32
-//   n2 = bf16(rms_norm(h, g2)); g, u = n2 W{g,u}^T   reng_hip_rms_norm_bf16, (fp8 GEMV)
+//   h  = x + a Wo^T; n2 = bf16(rms_norm(h, g2))     (fp8 GEMV), reng_hip_add_rms_norm_bf16
+//   g, u = n2 W{g,u}^T                               (fp8 GEMV)
 //   y  = h + (silu(g) * u) Wd^T                      reng_hip_silu_mul_bf16, (fp8 GEMV), add
 //
 // The semantics are the reference's CPU decoder layer, causal, in its Llama
@@ -54,17 +54,62 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 }
 
 // out[r, c] = bf16(x[r, c] * inv_r * g[c]), inv_r = 1 / sqrt(mean_c x[r, c]^2 + eps)
-// (rms_norm_cpu, ops.rs:49-72). One block per row.
-__global__ __launch_bounds__(256) void rms_norm_bf16(const float *__restrict__ x, const float *__restrict__ g,
-                                                     uint32_t cols, float eps, uint16_t *__restrict__ out) {
-    __shared__ float red[4];
-    const float *xr = x + (size_t)blockIdx.x * cols;
+// (rms_norm_cpu, ops.rs:49-72). With ADD the row normalised is h = x + d (d a
+// bf16 branch output), which is also written out. One 1024-thread workgroup
+// per row; VEC moves four columns per thread and access (cols % 4 == 0,
+// aligned rows), so a row of up to 4096 columns is one load per thread.
+constexpr int NORM_THREADS = 1024;
+
+template <bool VEC, bool ADD>
+__global__ __launch_bounds__(NORM_THREADS) void rms_norm_rows(const float *__restrict__ x,
+                                                              const uint16_t *__restrict__ d,
+                                                              const float *__restrict__ g, uint32_t cols, float eps,
+                                                              float *__restrict__ h, uint16_t *__restrict__ out) {
+    __shared__ float red[NORM_THREADS / 64];
+    const size_t base = (size_t)blockIdx.x * cols;
+    const float *xr = x + base;
+    float *hr = ADD ? h + base : nullptr;
+    const uint16_t *dr = ADD ? d + base : nullptr;
+    uint16_t *orow = out + base;
     float ss = 0.0f;
-    for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) ss += xr[c] * xr[c];
+    if constexpr (VEC) {
+        for (uint32_t c = threadIdx.x * 4; c < cols; c += NORM_THREADS * 4) {
+            float4 v = *reinterpret_cast<const float4 *>(xr + c);
+            if constexpr (ADD) {
+                const u32x2 w = *reinterpret_cast<const u32x2 *>(dr + c);
+                v.x += __uint_as_float(w.x << 16);
+                v.y += __uint_as_float(w.x & 0xffff0000u);
+                v.z += __uint_as_float(w.y << 16);
+                v.w += __uint_as_float(w.y & 0xffff0000u);
+                *reinterpret_cast<float4 *>(hr + c) = v;
+            }
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    } else {
+        for (uint32_t c = threadIdx.x; c < cols; c += NORM_THREADS) {
+            float v = xr[c];
+            if constexpr (ADD) {
+                v += bf16_f32(dr[c]);
+                hr[c] = v;
+            }
+            ss += v * v;
+        }
+    }
     const float ms = block_sum(ss, red) / (float)cols;
     const float inv = 1.0f / sqrtf(ms + eps);
-    uint16_t *orow = out + (size_t)blockIdx.x * cols;
-    for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) orow[c] = f32_bf16(xr[c] * inv * g[c]);
+    // The second pass reads back what this thread read (or wrote) in the first.
+    const float *src = ADD ? hr : xr;
+    if constexpr (VEC) {
+        for (uint32_t c = threadIdx.x * 4; c < cols; c += NORM_THREADS * 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + c);
+            const float4 gv = *reinterpret_cast<const float4 *>(g + c);
+            const uint32_t lo = f32_bf16(v.x * inv * gv.x) | ((uint32_t)f32_bf16(v.y * inv * gv.y) << 16);
+            const uint32_t hi = f32_bf16(v.z * inv * gv.z) | ((uint32_t)f32_bf16(v.w * inv * gv.w) << 16);
+            *reinterpret_cast<u32x2 *>(orow + c) = u32x2{lo, hi};
+        }
+    } else {
+        for (uint32_t c = threadIdx.x; c < cols; c += NORM_THREADS) orow[c] = f32_bf16(src[c] * inv * g[c]);
+    }
 }
 
 // Rotate-half RoPE of one position (rope_cpu, ops.rs:118-135): for d < half,
@@ -379,6 +424,26 @@ namespace {
 hipStream_t stream_of(void *s) { return static_cast<hipStream_t>(s); }
 }
 
+namespace {
+
+template <bool ADD>
+int launch_norm(const float *x, const uint16_t *d, const float *gamma, size_t rows, size_t cols, float eps, float *h,
+                uint16_t *out, hipStream_t st) {
+    const uintptr_t a16 = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
+                          reinterpret_cast<uintptr_t>(h);
+    const uintptr_t a8 = reinterpret_cast<uintptr_t>(d) | reinterpret_cast<uintptr_t>(out);
+    const bool vec = cols % 4 == 0 && (a16 & 15) == 0 && (a8 & 7) == 0;
+    if (vec)
+        hipLaunchKernelGGL((rms_norm_rows<true, ADD>), dim3((unsigned)rows), dim3(NORM_THREADS), 0, st, x, d, gamma,
+                           (uint32_t)cols, eps, h, out);
+    else
+        hipLaunchKernelGGL((rms_norm_rows<false, ADD>), dim3((unsigned)rows), dim3(NORM_THREADS), 0, st, x, d, gamma,
+                           (uint32_t)cols, eps, h, out);
+    return check_launch("rms_norm_rows");
+}
+
+}  // namespace
+
 RENG_HIP_API int reng_hip_rms_norm_bf16(const float *x, const float *gamma, size_t rows, size_t cols, float eps,
                                         uint16_t *out, void *stream) {
     clear_error();
@@ -386,9 +451,17 @@ RENG_HIP_API int reng_hip_rms_norm_bf16(const float *x, const float *gamma, size
     RENG_REQUIRE(rows <= 0x7fffffff && cols <= 0x7fffffff, "dimension too large");
     RENG_REQUIRE(x && gamma && out, "null pointer");
     RENG_REQUIRE(eps >= 0.0f, "eps %g is negative", (double)eps);
-    hipLaunchKernelGGL(rms_norm_bf16, dim3((unsigned)rows), dim3(256), 0, stream_of(stream), x, gamma,
-                       (uint32_t)cols, eps, out);
-    return check_launch("rms_norm_bf16");
+    return launch_norm<false>(x, nullptr, gamma, rows, cols, eps, nullptr, out, stream_of(stream));
+}
+
+RENG_HIP_API int reng_hip_add_rms_norm_bf16(const float *x, const uint16_t *d, const float *gamma, size_t rows,
+                                            size_t cols, float eps, float *h, uint16_t *out, void *stream) {
+    clear_error();
+    RENG_REQUIRE(rows > 0 && cols > 0, "empty shape %zu x %zu", rows, cols);
+    RENG_REQUIRE(rows <= 0x7fffffff && cols <= 0x7fffffff, "dimension too large");
+    RENG_REQUIRE(x && d && gamma && h && out, "null pointer");
+    RENG_REQUIRE(eps >= 0.0f, "eps %g is negative", (double)eps);
+    return launch_norm<true>(x, d, gamma, rows, cols, eps, h, out, stream_of(stream));
 }
 
 RENG_HIP_API int reng_hip_rope_append(uint16_t *q, const uint16_t *k, const uint16_t *v, size_t n_heads,

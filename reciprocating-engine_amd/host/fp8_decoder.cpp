@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
+#include <initializer_list>
 #include <string>
 
 #include "../../include/reng_hip.h"
@@ -62,31 +63,52 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
     };
     try {
         const size_t qd = nh_ * hd_, kvd = nkv_ * hd_;
-        auto mat = [&](const reng_fp8::Quantized &q, size_t rows, size_t cols, const char *name) {
+        auto check = [&](const reng_fp8::Quantized &q, size_t rows, size_t cols, const char *name) {
             if (q.rows != rows || q.cols != cols)
                 throw Error(std::string("Fp8Decoder: ") + name + " is " + std::to_string(q.rows) + " x " +
                             std::to_string(q.cols) + ", the config implies " + std::to_string(rows) + " x " +
                             std::to_string(cols));
             if (cols % 16 != 0) throw Error(std::string("Fp8Decoder: ") + name + " width is not a multiple of 16");
+        };
+        // Projections of one input row are one GEMV over their rows stacked in
+        // order (q, k, v; gate, up): each output row is its own matrix's row.
+        auto mat = [&](std::initializer_list<const reng_fp8::Quantized *> parts) {
+            const reng_fp8::Quantized &first = **parts.begin();
             Mat m;
-            m.codes = static_cast<uint8_t *>(upload(q.codes.data(), q.codes.size()));
-            m.scales = static_cast<float *>(upload(q.scales.data(), q.scales.size() * sizeof(float)));
-            m.rows = rows;
-            m.cols = cols;
-            m.format = abi_format(q.format);
+            m.cols = first.cols;
+            m.format = abi_format(first.format);
+            for (const reng_fp8::Quantized *q : parts) {
+                if (abi_format(q->format) != m.format)
+                    throw Error("Fp8Decoder: projections of one input row carry different fp8 formats");
+                m.rows += q->rows;
+            }
+            m.codes = static_cast<uint8_t *>(dev(m.rows * m.cols));
+            m.scales = static_cast<float *>(dev(m.rows * sizeof(float)));
+            size_t r0 = 0;
+            for (const reng_fp8::Quantized *q : parts) {
+                hip_ok(hipMemcpy(m.codes + r0 * m.cols, q->codes.data(), q->codes.size(), hipMemcpyHostToDevice),
+                       "hipMemcpy");
+                hip_ok(hipMemcpy(m.scales + r0, q->scales.data(), q->rows * sizeof(float), hipMemcpyHostToDevice),
+                       "hipMemcpy");
+                r0 += q->rows;
+            }
             return m;
         };
         for (size_t li = 0; li < w.layers.size(); ++li) {
             const LayerFp8 &f = (*w.fp8)[li];
             const LayerTensors &t = w.layers[li];
+            check(f.wq, qd, hidden_, "wq");
+            check(f.wk, kvd, hidden_, "wk");
+            check(f.wv, kvd, hidden_, "wv");
+            check(f.wo, hidden_, qd, "wo");
+            check(f.wg, inter_, hidden_, "wg");
+            check(f.wu, inter_, hidden_, "wu");
+            check(f.wd, hidden_, inter_, "wd");
             Layer L;
-            L.wq = mat(f.wq, qd, hidden_, "wq");
-            L.wk = mat(f.wk, kvd, hidden_, "wk");
-            L.wv = mat(f.wv, kvd, hidden_, "wv");
-            L.wo = mat(f.wo, hidden_, qd, "wo");
-            L.wg = mat(f.wg, inter_, hidden_, "wg");
-            L.wu = mat(f.wu, inter_, hidden_, "wu");
-            L.wd = mat(f.wd, hidden_, inter_, "wd");
+            L.wqkv = mat({&f.wq, &f.wk, &f.wv});
+            L.wo = mat({&f.wo});
+            L.wgu = mat({&f.wg, &f.wu});
+            L.wd = mat({&f.wd});
             if (t.g1.size() != hidden_ || t.g2.size() != hidden_) throw Error("Fp8Decoder: norm gains are not [hidden]");
             L.g1 = static_cast<float *>(upload(t.g1.data(), hidden_ * sizeof(float)));
             L.g2 = static_cast<float *>(upload(t.g2.data(), hidden_ * sizeof(float)));
@@ -111,13 +133,13 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
         h_ = static_cast<float *>(dev(hidden_ * 4));
         // bf16 buffers 16-byte aligned (hipMalloc) for the GEMV's inputs.
         n_ = static_cast<uint16_t *>(dev(hidden_ * 2));
-        q_ = static_cast<uint16_t *>(dev(qd * 2));
-        k_ = static_cast<uint16_t *>(dev(kvd * 2));
-        v_ = static_cast<uint16_t *>(dev(kvd * 2));
+        q_ = static_cast<uint16_t *>(dev((qd + 2 * kvd) * 2));   // q | k | v, one GEMV's output
+        k_ = q_ + qd;
+        v_ = k_ + kvd;
         a_ = static_cast<uint16_t *>(dev(qd * 2));
         o_ = static_cast<uint16_t *>(dev(hidden_ * 2));
-        gate_ = static_cast<uint16_t *>(dev(inter_ * 2));
-        up_ = static_cast<uint16_t *>(dev(inter_ * 2));
+        gate_ = static_cast<uint16_t *>(dev(2 * inter_ * 2));   // gate | up
+        up_ = gate_ + inter_;
         act_ = static_cast<uint16_t *>(dev(inter_ * 2));
         down_ = static_cast<uint16_t *>(dev(hidden_ * 2));
         attn_ws_bytes_ = reng_hip_attention_workspace_bytes(nh_, hd_, max_pos_);
@@ -146,18 +168,14 @@ void Fp8Decoder::step_device(size_t li, const float *x, float *y, size_t pos, vo
     if (pos >= max_pos_) throw Error("Fp8Decoder: position " + std::to_string(pos) + " is past the cache");
     const size_t kvd = nkv_ * hd_;
     abi_ok(reng_hip_rms_norm_bf16(x, L.g1, 1, hidden_, eps_, n_, stream));
-    gemv(L.wq, n_, q_, stream);
-    gemv(L.wk, n_, k_, stream);
-    gemv(L.wv, n_, v_, stream);
+    gemv(L.wqkv, n_, q_, stream);
     abi_ok(reng_hip_rope_append(q_, k_, v_, nh_, nkv_, hd_, sin_ + pos * hd_, cos_ + pos * hd_,
                                 L.kcache + pos * kvd, L.vcache + pos * kvd, stream));
     abi_ok(reng_hip_attention_decode_split(q_, L.kcache, L.vcache, nh_, nkv_, hd_, pos + 1, scale_, attn_ws_,
                                            attn_ws_bytes_, a_, stream));
     gemv(L.wo, a_, o_, stream);
-    abi_ok(reng_hip_add_bf16_f32(x, o_, hidden_, h_, stream));
-    abi_ok(reng_hip_rms_norm_bf16(h_, L.g2, 1, hidden_, eps_, n_, stream));
-    gemv(L.wg, n_, gate_, stream);
-    gemv(L.wu, n_, up_, stream);
+    abi_ok(reng_hip_add_rms_norm_bf16(x, o_, L.g2, 1, hidden_, eps_, h_, n_, stream));
+    gemv(L.wgu, n_, gate_, stream);
     abi_ok(reng_hip_silu_mul_bf16(gate_, up_, inter_, act_, stream));
     gemv(L.wd, act_, down_, stream);
     abi_ok(reng_hip_add_bf16_f32(h_, down_, hidden_, y, stream));

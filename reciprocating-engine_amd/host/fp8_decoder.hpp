@@ -1,6 +1,7 @@
 // fp8_decoder.hpp - the device consumer of LlamaWeights::fp8: one decode step
 // (one token) of a Llama decoder layer whose seven projections are the fp8
-// GEMV over the layer's codes and per-row scales.
+// GEMV over the layer's codes and per-row scales (q, k and v as one GEMV over
+// their stacked rows, gate and up as another).
 //
 // The reference quantizes on the host and then refuses at the point where the
 // codes would meet a device layer (layer_views, crates/reng-model/src/lib.rs:
@@ -59,7 +60,7 @@ class Fp8Decoder {
         int format = 0;
     };
     struct Layer {
-        Mat wq, wk, wv, wo, wg, wu, wd;
+        Mat wqkv, wo, wgu, wd;   // q, k, v rows stacked; gate, up rows stacked
         float *g1 = nullptr, *g2 = nullptr;
         uint16_t *kcache = nullptr, *vcache = nullptr;
         size_t pos = 0;

@@ -60,6 +60,7 @@ SIGNATURES = {
     "reng_hip_gemm_fp8_scaled": (_I, [_P, _I, _P, _SZ, _P, _I, _P, _SZ, _SZ, _SZ, _SZ, _P, _P]),
     "reng_hip_verify_hw_convert": (_I, [_I, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32)]),
     "reng_hip_rms_norm_bf16": (_I, [_P, _P, _SZ, _SZ, _F, _P, _P]),
+    "reng_hip_add_rms_norm_bf16": (_I, [_P, _P, _P, _SZ, _SZ, _F, _P, _P, _P]),
     "reng_hip_rope_append": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P]),
     "reng_hip_attention_decode": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _P]),
     "reng_hip_attention_workspace_bytes": (_SZ, [_SZ, _SZ, _SZ]),
@@ -328,6 +329,19 @@ def rms_norm_bf16(x, gamma, rows, cols, eps, out=None):
     _check(lib().reng_hip_rms_norm_bf16(_dev(x, "x"), _dev(gamma, "gamma"), rows, cols, eps, _dev(out, "out"),
                                         _stream()))
     return out
+
+
+def add_rms_norm_bf16(x, d, gamma, rows, cols, eps, h=None, out=None):
+    """h = x + d (f32) and out = bf16(rms_norm(h) * gamma); returns (h, out)."""
+    import torch
+
+    if h is None:
+        h = torch.empty(rows * cols, dtype=torch.float32, device=x.device)
+    if out is None:
+        out = torch.empty(rows * cols, dtype=torch.bfloat16, device=x.device)
+    _check(lib().reng_hip_add_rms_norm_bf16(_dev(x, "x"), _dev(d, "d"), _dev(gamma, "gamma"), rows, cols, eps,
+                                            _dev(h, "h"), _dev(out, "out"), _stream()))
+    return h, out
 
 
 def rope_append(q, k, v, n_heads, n_kv_heads, head_dim, sin_row, cos_row, k_row, v_row):

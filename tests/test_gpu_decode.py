@@ -204,6 +204,8 @@ def test_decode_step_entry_points_refuse_bad_arguments():
     assert lib.reng_hip_rms_norm_bf16(None, p, 1, 8, 1e-5, p, None) == R.EINVAL
     assert lib.reng_hip_rms_norm_bf16(p, p, 0, 8, 1e-5, p, None) == R.EINVAL
     assert lib.reng_hip_rms_norm_bf16(p, p, 1, 8, -1.0, p, None) == R.EINVAL
+    assert lib.reng_hip_add_rms_norm_bf16(p, None, p, 1, 8, 1e-5, p, p, None) == R.EINVAL
+    assert lib.reng_hip_add_rms_norm_bf16(p, p, p, 1, 0, 1e-5, p, p, None) == R.EINVAL
     assert lib.reng_hip_rope_append(p, p, p, 6, 4, 64, p, p, p, p, None) == R.EINVAL       # 6 % 4
     assert lib.reng_hip_rope_append(p, p, p, 4, 2, 63, p, p, p, p, None) == R.EINVAL       # odd head_dim
     assert lib.reng_hip_attention_decode(p, p, p, 4, 2, 64, 0, 1.0, p, None) == R.EINVAL   # empty cache
@@ -236,11 +238,20 @@ def test_decode_step_kernels_against_numpy():
     rng = np.random.default_rng(21)
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
-    # RMSNorm over rows that are not a multiple of the block.
-    x = rng.standard_normal((3, 1000)).astype(np.float32) * 3
-    g = (1 + rng.standard_normal(1000) * 0.1).astype(np.float32)
-    got = bf16_f32(bits(R.rms_norm_bf16(dev(x), dev(g), 3, 1000, 1e-5))).reshape(3, 1000)
-    assert O.rel_l2(got.ravel(), L.rms_norm(x, g, 1e-5).ravel()) < 4e-3
+    # RMSNorm over rows that are not a multiple of the block: four columns per
+    # thread (cols % 4 == 0) and one (999), one and two passes of the block.
+    for rows, cols in ((3, 1000), (2, 999), (1, 4096), (1, 8192), (2, 12)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+        g = (1 + rng.standard_normal(cols) * 0.1).astype(np.float32)
+        got = bf16_f32(bits(R.rms_norm_bf16(dev(x), dev(g), rows, cols, 1e-5))).reshape(rows, cols)
+        assert O.rel_l2(got.ravel(), L.rms_norm(x, g, 1e-5).ravel()) < 4e-3, (rows, cols)
+        # h = x + d, then the norm of h
+        d = bf16_bits(rng.standard_normal((rows, cols)).astype(np.float32))
+        h, got = R.add_rms_norm_bf16(dev(x), dev(d.view(np.int16)), dev(g), rows, cols, 1e-5)
+        want_h = x + bf16_f32(d)
+        assert np.array_equal(h.cpu().numpy().reshape(rows, cols), want_h), (rows, cols)
+        got = bf16_f32(bits(got)).reshape(rows, cols)
+        assert O.rel_l2(got.ravel(), L.rms_norm(want_h, g, 1e-5).ravel()) < 4e-3, (rows, cols)
     # RoPE + append at position 5, 6 q heads over 2 kv heads.
     nh, nkv, hd, pos = 6, 2, 64, 5
     sin, cos = L.rope_caches(8, hd, 10000.0)
