@@ -185,6 +185,24 @@ RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const 
 RENG_HIP_API int reng_hip_rms_norm_bf16(const float *x, const float *gamma, size_t rows, size_t cols, float eps,
                                         uint16_t *out, void *stream);
 
+/* reng_hip_gemm_w8a16 at M = 1 with the residual add as its epilogue:
+ * y[n] = residual[n] + bf16(scales[n] * sum_k x[k] * decode(codes[n, k])),
+ * f32 residual and y [N] (y may be residual). Bit-identical to
+ * reng_hip_gemm_w8a16 (M = 1) then reng_hip_add_bf16_f32. Same argument rules
+ * as reng_hip_gemm_w8a16. */
+RENG_HIP_API int reng_hip_gemv_w8a16_residual(const uint16_t *x, const uint8_t *codes, const float *scales,
+                                              size_t N, size_t K, int format, const float *residual, float *y,
+                                              void *stream);
+
+/* A SwiGLU gate and up projection as one GEMV (M = 1) over rows in pairs:
+ * row 2i of codes / scales is gate row i, row 2i + 1 up row i (N = 2 *
+ * intermediate), and y[i] = bf16(silu(g_i) * u_i) with g_i, u_i the bf16
+ * outputs of the two rows, y bf16 [N / 2]. Bit-identical to
+ * reng_hip_gemm_w8a16 (M = 1) over each matrix then reng_hip_silu_mul_bf16.
+ * N even; otherwise as reng_hip_gemm_w8a16. */
+RENG_HIP_API int reng_hip_gemv_w8a16_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales,
+                                            size_t N, size_t K, int format, uint16_t *y, void *stream);
+
 /* h = x + d and out = bf16(rms_norm(h) * gamma) in one pass, x and h f32, d
  * bf16 [rows, cols] (a branch output added to the residual stream, then the
  * next sublayer's RMSNorm; h must not overlap x or d). */

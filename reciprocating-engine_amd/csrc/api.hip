@@ -295,6 +295,40 @@ RENG_HIP_API int reng_hip_gemm_w8a16(const uint16_t *x, const uint8_t *codes, co
                         as_stream(stream));
 }
 
+namespace {
+
+int gemv_epi_args(const uint16_t *x, const uint8_t *codes, size_t N, size_t K, int format) {
+    RENG_REQUIRE(valid_format(format), "unknown fp8 format %d", format);
+    RENG_REQUIRE(N > 0 && K > 0, "empty product 1 x %zu x %zu", N, K);
+    RENG_REQUIRE(K % 16 == 0, "K = %zu is not a multiple of 16", K);
+    RENG_REQUIRE(N <= 0x7fffffff && K <= 0x7fffffff, "dimension too large");
+    RENG_REQUIRE(x && codes, "null pointer");
+    RENG_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(codes)) & 15) == 0,
+                 "x and codes must be 16-byte aligned");
+    return RENG_HIP_OK;
+}
+
+}  // namespace
+
+RENG_HIP_API int reng_hip_gemv_w8a16_residual(const uint16_t *x, const uint8_t *codes, const float *scales,
+                                              size_t N, size_t K, int format, const float *residual, float *y,
+                                              void *stream) {
+    clear_error();
+    if (int rc = gemv_epi_args(x, codes, N, K, format)) return rc;
+    RENG_REQUIRE(residual && y, "null pointer");
+    return launch_gemv_residual(x, codes, scales, (uint32_t)N, (uint32_t)K, format, residual, y,
+                                as_stream(stream));
+}
+
+RENG_HIP_API int reng_hip_gemv_w8a16_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales,
+                                            size_t N, size_t K, int format, uint16_t *y, void *stream) {
+    clear_error();
+    if (int rc = gemv_epi_args(x, codes, N, K, format)) return rc;
+    RENG_REQUIRE(N % 2 == 0, "N = %zu rows do not form (gate, up) pairs", N);
+    RENG_REQUIRE(y, "null pointer");
+    return launch_gemv_swiglu(x, codes, scales, (uint32_t)N, (uint32_t)K, format, y, as_stream(stream));
+}
+
 RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const float *scale_a,
                                           size_t n_scale_a, const uint8_t *b, int b_format,
                                           const float *scale_b, size_t n_scale_b, size_t M,

@@ -9,6 +9,12 @@ namespace reng {
 
 int launch_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                  uint32_t N, uint32_t K, int format, uint16_t *y, hipStream_t st);
+// M = 1 with a fused epilogue: f32 y[n] = res[n] + bf16((W x)[n]) (residual), or
+// over rows in (gate, up) pairs, y[i] = bf16(silu(bf16 (W x)[2i]) * bf16 (W x)[2i + 1]) (N even).
+int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                         int format, const float *res, float *y, hipStream_t st);
+int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                       int format, uint16_t *y, hipStream_t st);
 // 4 < M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st);

@@ -1,7 +1,8 @@
 // gemm.hip - consumers of the quantizer's codes on CDNA4 (gfx950).
 //
 // 1. gemv_w8a16     (M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
-//                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]).
+//                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]); with
+//                    M = 1 also a residual-add epilogue and a SwiGLU-pair one.
 //    Streams the codes once with 16-byte loads, decodes in registers
 //    (v_cvt_pk_f32_fp8 / _bf8), f32 FMA, one wave per output row.
 // 2. The other M <= 64: the same product on bf16 MFMA with the codes and the
@@ -85,17 +86,39 @@ __device__ __forceinline__ void decode16(const u32x4 &q, uint32_t (&w)[8]) {
 // are staged once per block in LDS as bf16 (XLDS) or read through the caches.
 // Codes decode to bf16 pairs in registers and meet the activation in
 // v_dot2_f32_bf16 (f32 accumulation).
-template <int F, int M, int CPL, bool XLDS, bool RAGGED>
+//
+// Epilogues (M = 1): EPI_RESID writes f32 yres[n] = res[n] + bf16(y[n]) (a
+// projection and its residual add); EPI_SWIGLU takes rows in (gate, up) pairs
+// (row 2i of the matrix is gate row i, row 2i + 1 up row i), a wave computes
+// both rows of a pair, and y[i] = bf16(silu(bf16 gate) * bf16 up). Each is the
+// arithmetic of add_bf16_f32 / silu_mul_bf16 (layer.hip) after the plain
+// GEMV: a row's sum does not depend on which wave computes it.
+enum { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+
+__device__ __forceinline__ uint16_t silu_mul_bits(uint32_t g, uint32_t u) {
+    const float gv = __uint_as_float(g << 16), uv = __uint_as_float(u << 16);
+    return (uint16_t)f32_to_bf16_bits(gv / (1.0f + expf(-gv)) * uv);
+}
+
+template <int F, int M, int CPL, bool XLDS, bool RAGGED, int EPI = EPI_PLAIN>
 __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x,
                                                   const uint8_t *__restrict__ codes,
                                                   const float *__restrict__ scales, uint32_t N,
-                                                  uint32_t K, uint16_t *__restrict__ y) {
+                                                  uint32_t K, uint16_t *__restrict__ y, const float *res,
+                                                  float *yres) {
+    static_assert(EPI == EPI_PLAIN || M == 1, "the fused epilogues take one activation row");
+    constexpr bool PAIRS = EPI == EPI_SWIGLU;
     extern __shared__ __attribute__((aligned(16))) uint32_t xs[];
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t nch = K / 16;   // 16-code chunks per row
     const uint32_t waves = gridDim.x * (blockDim.x >> 6);
     const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (tid >> 6);
     const uint32_t gpr = (nch + 64 * CPL - 1) / (64 * CPL);   // groups per row
+    // The wave's i-th row: wave + i * waves, or with PAIRS row 2p + (i & 1) of
+    // pair p = wave + (i / 2) * waves.
+    auto row_at = [&](uint32_t i) -> uint32_t {
+        return PAIRS ? 2 * (wave + (i >> 1) * waves) + (i & 1) : wave + i * waves;
+    };
 
     // Loads are unconditional (indices clamped into the matrix) so the wait
     // before each use covers exactly the loads issued before it; a ragged
@@ -113,7 +136,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 
     // The first group's codes and the scales are requested before the
     // activation is staged.
-    uint32_t r = wave, gi = 0;
+    uint32_t r = row_at(0), gi = 0;
     u32x4 qn[CPL];
     // Lane j holds the scale of this wave's row ri + j (ri = rows done,
     // refilled every 64 rows), so an end-of-row multiply reads it with
@@ -121,10 +144,10 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
     uint32_t ri = 0;
     float sv = 1.0f;
     auto scales_from = [&](uint32_t first) {   // lanes past the last row repeat it (never read)
-        const uint32_t rr = wave + (first + lane) * waves;
+        const uint32_t rr = row_at(first + lane);
         sv = scales[rr < N ? rr : N - 1];
     };
-    if (wave < N) {
+    if (r < N) {
         load(r, gi, qn);
         if (scales) scales_from(0);
     }
@@ -134,7 +157,8 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
         for (uint32_t i = tid; i < M * nch * 2; i += blockDim.x) dst[i] = src[i];
         __syncthreads();
     }
-    if (wave >= N) return;
+    if (r >= N) return;
+    uint32_t gate_bits = 0;   // EPI_SWIGLU: the pair's gate, held until its up row ends
     float acc[M][2];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
@@ -146,7 +170,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
         uint32_t rn = r, gn = gi + 1;
         if (gn == gpr) {
             gn = 0;
-            rn = r + waves;
+            rn = PAIRS ? ((r & 1) ? r - 1 + 2 * waves : r + 1) : r + waves;
         }
         if (rn < N) load(rn, gn, qn);   // none past the wave's last row
 
@@ -189,7 +213,18 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 const float t = wave_sum_dpp(acc[m][0] + acc[m][1]);
-                if (lane == m) y[(size_t)m * N + r] = (uint16_t)f32_to_bf16_bits(t * s);
+                if constexpr (EPI == EPI_RESID) {
+                    if (lane == 0) yres[r] = res[r] + __uint_as_float(f32_to_bf16_bits(t * s) << 16);
+                } else if constexpr (EPI == EPI_SWIGLU) {
+                    const uint32_t b = f32_to_bf16_bits(t * s);
+                    if (r & 1) {
+                        if (lane == 0) y[r >> 1] = silu_mul_bits(gate_bits, b);
+                    } else {
+                        gate_bits = b;
+                    }
+                } else {
+                    if (lane == m) y[(size_t)m * N + r] = (uint16_t)f32_to_bf16_bits(t * s);
+                }
                 acc[m][0] = acc[m][1] = 0.0f;
             }
         }
@@ -240,6 +275,64 @@ float *split_workspace(size_t floats, hipStream_t st, int *rc) {
     return e.first;
 }
 
+// The GEMV's launch for M <= 4 rows: rows (or row groups of `unit`, which a
+// wave takes together) divide evenly over the waves, at most 16 waves per CU;
+// the activation is staged in LDS when it fits in 64 KB; 7 chunks per lane
+// when a row splits into whole groups of 7 (K a multiple of 7168, e.g.
+// 14336), else 4.
+struct GemvPlan {
+    static constexpr int threads = 512;
+    uint32_t blocks;
+    size_t lds;
+    bool xlds, cpl7, ragged;
+};
+
+GemvPlan gemv_plan(uint32_t M, uint32_t N, uint32_t K, uint32_t unit) {
+    GemvPlan p;
+    const uint32_t units = N / unit;
+    const uint32_t cap = (uint32_t)device_props().cus * 16;
+    const uint32_t rpw = (units + cap - 1) / cap;
+    const uint32_t waves = (units + rpw - 1) / rpw;
+    const size_t xbytes = (size_t)M * K * 2;
+    p.xlds = xbytes <= 64 * 1024;
+    p.blocks = (waves + GemvPlan::threads / 64 - 1) / (GemvPlan::threads / 64);
+    p.lds = p.xlds ? xbytes : 0;
+    p.cpl7 = (K / 16) % (64 * 7) == 0;
+    p.ragged = (K / 16) % (64 * (p.cpl7 ? 7 : 4)) != 0;
+    return p;
+}
+
+template <int F, int EPI>
+int launch_gemv_epi_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                      uint16_t *y, const float *res, float *yres, hipStream_t st) {
+    const GemvPlan p = gemv_plan(1, N, K, EPI == EPI_SWIGLU ? 2 : 1);
+#define RENG_GEMV_E(C, XL, RG)                                                                                  \
+    hipLaunchKernelGGL((gemv_w8a16<F, 1, C, XL, RG, EPI>), dim3(p.blocks), dim3(GemvPlan::threads), p.lds, st, x, \
+                       codes, scales, N, K, y, res, yres)
+#define RENG_GEMV_EX(C, RG) \
+    if (p.xlds) RENG_GEMV_E(C, true, RG); else RENG_GEMV_E(C, false, RG);
+    if (p.cpl7) { RENG_GEMV_EX(7, false) }
+    else if (p.ragged) { RENG_GEMV_EX(4, true) }
+    else { RENG_GEMV_EX(4, false) }
+#undef RENG_GEMV_EX
+#undef RENG_GEMV_E
+    return check_launch(EPI == EPI_SWIGLU ? "gemv_w8a16 (SwiGLU pairs)" : "gemv_w8a16 (residual)");
+}
+
+int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                         int format, const float *res, float *y, hipStream_t st) {
+    return format == RENG_HIP_E4M3
+               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, st)
+               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, st);
+}
+
+int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                       int format, uint16_t *y, hipStream_t st) {
+    return format == RENG_HIP_E4M3
+               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_SWIGLU>(x, codes, scales, N, K, y, nullptr, nullptr, st)
+               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_SWIGLU>(x, codes, scales, N, K, y, nullptr, nullptr, st);
+}
+
 template <int F>
 int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
@@ -261,23 +354,14 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     if (M >= 2 && M <= 4 && K % 128 == 0 && (M >= 3 || (size_t)M * K * 2 > 64 * 1024))
         return launch_skinny_mfma(x, codes, scales, M, N, K, F, y, st);
     if (M <= 4) {
-        // Rows divide evenly over the waves: at most 16 waves per CU, each
-        // taking rows_per_wave rows.
-        const uint32_t cap = (uint32_t)device_props().cus * 16;
-        const uint32_t rpw = (N + cap - 1) / cap;
-        const uint32_t waves = (N + rpw - 1) / rpw;
-        const size_t xbytes = (size_t)M * K * 2;
-        const bool xlds = xbytes <= 64 * 1024;
-        const int threads = 512;
-        const uint32_t blocks = (waves + threads / 64 - 1) / (threads / 64);
-        const size_t lds = xlds ? xbytes : 0;
-        // 7 chunks per lane when a row splits into whole groups of 7 (K a multiple
-        // of 7168, e.g. 14336), else 4.
-        const bool cpl7 = (K / 16) % (64 * 7) == 0;
-        const bool ragged = (K / 16) % (64 * (cpl7 ? 7 : 4)) != 0;
+        const GemvPlan p = gemv_plan(M, N, K, 1);
+        const uint32_t blocks = p.blocks;
+        const int threads = GemvPlan::threads;
+        const size_t lds = p.lds;
+        const bool xlds = p.xlds, cpl7 = p.cpl7, ragged = p.ragged;
 #define RENG_GEMV(MM, C, XL, RG)                                                                   \
     hipLaunchKernelGGL((gemv_w8a16<F, MM, C, XL, RG>), dim3(blocks), dim3(threads), lds, st, x, codes, \
-                       scales, N, K, y)
+                       scales, N, K, y, nullptr, nullptr)
 #define RENG_GEMV_X(MM, C, RG) \
     if (xlds) RENG_GEMV(MM, C, true, RG); else RENG_GEMV(MM, C, false, RG);
 #define RENG_GEMV_M(MM)                                  \

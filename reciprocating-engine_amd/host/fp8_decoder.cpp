@@ -71,9 +71,13 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
             if (cols % 16 != 0) throw Error(std::string("Fp8Decoder: ") + name + " width is not a multiple of 16");
         };
         // Projections of one input row are one GEMV over their rows stacked in
-        // order (q, k, v; gate, up): each output row is its own matrix's row.
-        auto mat = [&](std::initializer_list<const reng_fp8::Quantized *> parts) {
+        // order (q, k, v): each output row is its own matrix's row. With
+        // `pairs` two matrices of equal rows alternate instead (gate row i at
+        // 2i, up row i at 2i + 1), the layout of the SwiGLU GEMV.
+        auto mat = [&](std::initializer_list<const reng_fp8::Quantized *> parts, bool pairs = false) {
             const reng_fp8::Quantized &first = **parts.begin();
+            if (pairs && (parts.size() != 2 || parts.begin()[1]->rows != first.rows))
+                throw Error("Fp8Decoder: paired projections need two matrices of equal rows");
             Mat m;
             m.cols = first.cols;
             m.format = abi_format(first.format);
@@ -86,6 +90,16 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
             m.scales = static_cast<float *>(dev(m.rows * sizeof(float)));
             size_t r0 = 0;
             for (const reng_fp8::Quantized *q : parts) {
+                if (pairs) {   // rows r0, r0 + 2, ... of the interleaved matrix (r0 = 0, 1)
+                    hip_ok(hipMemcpy2D(m.codes + r0 * m.cols, 2 * m.cols, q->codes.data(), m.cols, m.cols, q->rows,
+                                       hipMemcpyHostToDevice),
+                           "hipMemcpy2D");
+                    hip_ok(hipMemcpy2D(m.scales + r0, 2 * sizeof(float), q->scales.data(), sizeof(float),
+                                       sizeof(float), q->rows, hipMemcpyHostToDevice),
+                           "hipMemcpy2D");
+                    r0 += 1;
+                    continue;
+                }
                 hip_ok(hipMemcpy(m.codes + r0 * m.cols, q->codes.data(), q->codes.size(), hipMemcpyHostToDevice),
                        "hipMemcpy");
                 hip_ok(hipMemcpy(m.scales + r0, q->scales.data(), q->rows * sizeof(float), hipMemcpyHostToDevice),
@@ -107,7 +121,7 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
             Layer L;
             L.wqkv = mat({&f.wq, &f.wk, &f.wv});
             L.wo = mat({&f.wo});
-            L.wgu = mat({&f.wg, &f.wu});
+            L.wgu = mat({&f.wg, &f.wu}, true);
             L.wd = mat({&f.wd});
             if (t.g1.size() != hidden_ || t.g2.size() != hidden_) throw Error("Fp8Decoder: norm gains are not [hidden]");
             L.g1 = static_cast<float *>(upload(t.g1.data(), hidden_ * sizeof(float)));
@@ -138,10 +152,7 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
         v_ = k_ + kvd;
         a_ = static_cast<uint16_t *>(dev(qd * 2));
         o_ = static_cast<uint16_t *>(dev(hidden_ * 2));
-        gate_ = static_cast<uint16_t *>(dev(2 * inter_ * 2));   // gate | up
-        up_ = gate_ + inter_;
         act_ = static_cast<uint16_t *>(dev(inter_ * 2));
-        down_ = static_cast<uint16_t *>(dev(hidden_ * 2));
         attn_ws_bytes_ = reng_hip_attention_workspace_bytes(nh_, hd_, max_pos_);
         attn_ws_ = dev(attn_ws_bytes_);
     } catch (...) {
@@ -175,10 +186,10 @@ void Fp8Decoder::step_device(size_t li, const float *x, float *y, size_t pos, vo
                                            attn_ws_bytes_, a_, stream));
     gemv(L.wo, a_, o_, stream);
     abi_ok(reng_hip_add_rms_norm_bf16(x, o_, L.g2, 1, hidden_, eps_, h_, n_, stream));
-    gemv(L.wgu, n_, gate_, stream);
-    abi_ok(reng_hip_silu_mul_bf16(gate_, up_, inter_, act_, stream));
-    gemv(L.wd, act_, down_, stream);
-    abi_ok(reng_hip_add_bf16_f32(h_, down_, hidden_, y, stream));
+    abi_ok(reng_hip_gemv_w8a16_swiglu(n_, L.wgu.codes, L.wgu.scales, L.wgu.rows, L.wgu.cols, L.wgu.format, act_,
+                                      stream));
+    abi_ok(reng_hip_gemv_w8a16_residual(act_, L.wd.codes, L.wd.scales, L.wd.rows, L.wd.cols, L.wd.format, h_, y,
+                                        stream));
     ++L.pos;
 }
 

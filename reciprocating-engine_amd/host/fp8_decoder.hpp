@@ -1,7 +1,9 @@
 // fp8_decoder.hpp - the device consumer of LlamaWeights::fp8: one decode step
 // (one token) of a Llama decoder layer whose seven projections are the fp8
 // GEMV over the layer's codes and per-row scales (q, k and v as one GEMV over
-// their stacked rows, gate and up as another).
+// their stacked rows; gate and up as one over their rows alternating, with
+// silu(gate) * up as its epilogue; down with the residual add as its
+// epilogue).
 //
 // The reference quantizes on the host and then refuses at the point where the
 // codes would meet a device layer (layer_views, crates/reng-model/src/lib.rs:
@@ -60,7 +62,7 @@ class Fp8Decoder {
         int format = 0;
     };
     struct Layer {
-        Mat wqkv, wo, wgu, wd;   // q, k, v rows stacked; gate, up rows stacked
+        Mat wqkv, wo, wgu, wd;   // q, k, v rows stacked; gate, up rows alternating
         float *g1 = nullptr, *g2 = nullptr;
         uint16_t *kcache = nullptr, *vcache = nullptr;
         size_t pos = 0;
@@ -75,7 +77,7 @@ class Fp8Decoder {
     // scratch: residual f32 rows, bf16 GEMV inputs and outputs
     float *x_ = nullptr, *h_ = nullptr;
     uint16_t *n_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *a_ = nullptr, *o_ = nullptr;
-    uint16_t *gate_ = nullptr, *up_ = nullptr, *act_ = nullptr, *down_ = nullptr;
+    uint16_t *act_ = nullptr;
     // the split attention's partial outputs (one layer at a time)
     void *attn_ws_ = nullptr;
     size_t attn_ws_bytes_ = 0;

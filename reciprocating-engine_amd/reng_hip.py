@@ -61,6 +61,8 @@ SIGNATURES = {
     "reng_hip_verify_hw_convert": (_I, [_I, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32)]),
     "reng_hip_rms_norm_bf16": (_I, [_P, _P, _SZ, _SZ, _F, _P, _P]),
     "reng_hip_add_rms_norm_bf16": (_I, [_P, _P, _P, _SZ, _SZ, _F, _P, _P, _P]),
+    "reng_hip_gemv_w8a16_residual": (_I, [_P, _P, _P, _SZ, _SZ, _I, _P, _P, _P]),
+    "reng_hip_gemv_w8a16_swiglu": (_I, [_P, _P, _P, _SZ, _SZ, _I, _P, _P]),
     "reng_hip_rope_append": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P]),
     "reng_hip_attention_decode": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _P]),
     "reng_hip_attention_workspace_bytes": (_SZ, [_SZ, _SZ, _SZ]),
@@ -328,6 +330,31 @@ def rms_norm_bf16(x, gamma, rows, cols, eps, out=None):
         out = torch.empty(rows * cols, dtype=torch.bfloat16, device=x.device)
     _check(lib().reng_hip_rms_norm_bf16(_dev(x, "x"), _dev(gamma, "gamma"), rows, cols, eps, _dev(out, "out"),
                                         _stream()))
+    return out
+
+
+def gemv_residual(x, codes, scales, n, k, fmt, residual, out=None):
+    """f32 out[n] = residual + bf16(x . (decode(codes[n, k]) * scales)^T), x bf16 [k]."""
+    import torch
+
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=x.device)
+    _check(lib().reng_hip_gemv_w8a16_residual(_dev(x, "x"), _dev(codes, "codes"),
+                                              None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt),
+                                              _dev(residual, "residual"), _dev(out, "out"), _stream()))
+    return out
+
+
+def gemv_swiglu(x, codes, scales, n, k, fmt, out=None):
+    """bf16 out[n / 2] = silu(gate) * up over codes whose rows alternate gate,
+    up (row 2i gate row i, row 2i + 1 up row i)."""
+    import torch
+
+    if out is None:
+        out = torch.empty(n // 2, dtype=torch.bfloat16, device=x.device)
+    _check(lib().reng_hip_gemv_w8a16_swiglu(_dev(x, "x"), _dev(codes, "codes"),
+                                            None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt),
+                                            _dev(out, "out"), _stream()))
     return out
 
 

@@ -226,6 +226,14 @@ def test_decode_step_entry_points_refuse_bad_arguments():
     assert lib.reng_hip_attention_decode_split(p, p, p, 4, 2, 64, 700, 1.0, None, need, p, None) == R.EINVAL
     assert lib.reng_hip_attention_decode_split(p, p, p, 4, 2, 64, 0, 1.0, p, need, p, None) == R.EINVAL
     assert lib.reng_hip_silu_mul_bf16(p, p, 0, p, None) == R.EINVAL
+    rs, sw = lib.reng_hip_gemv_w8a16_residual, lib.reng_hip_gemv_w8a16_swiglu
+    assert rs(p, p, p, 8, 40, R.E4M3, p, p, None) == R.EINVAL                            # K % 16
+    assert rs(p, p, p, 8, 64, 7, p, p, None) == R.EINVAL                                 # format
+    assert rs(ctypes.c_void_p(24), p, p, 8, 64, R.E4M3, p, p, None) == R.EINVAL          # misaligned x
+    assert rs(p, p, p, 8, 64, R.E4M3, None, p, None) == R.EINVAL                         # no residual
+    assert sw(p, p, p, 7, 64, R.E4M3, p, None) == R.EINVAL                               # odd N
+    assert b"pairs" in lib.reng_hip_last_error()
+    assert sw(p, p, p, 0, 64, R.E4M3, p, None) == R.EINVAL
     assert lib.reng_hip_add_bf16_f32(p, None, 4, p, None) == R.EINVAL
 
 
@@ -295,6 +303,53 @@ def test_decode_step_kernels_against_numpy():
     xr = rng.standard_normal(999).astype(np.float32)
     out = R.add_bf16_f32(dev(xr), dev(up.view(np.int16)), 999).cpu().numpy()
     assert np.array_equal(out, xr + bf16_f32(up))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_gemv_epilogues_equal_the_unfused_steps(fmt):
+    """The residual epilogue against gemm_w8a16 (M = 1) then add_bf16_f32, and
+    the SwiGLU-pair epilogue against gemm_w8a16 over gate and over up then
+    silu_mul_bf16, bit for bit: K = 14336 (7 chunks per lane), 4096 (4), 1008
+    (a ragged last group) and 40000 (activation read through the caches, not
+    LDS); row counts that do not divide over the waves; unit scales; the
+    residual output written over its input."""
+    import torch
+
+    import reng_hip as R
+
+    rng = np.random.default_rng(5 if fmt == "e4m3" else 6)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def quant(n, k):
+        w = bf16_bits(rng.standard_normal((n, k)).astype(np.float32) * 0.05)
+        return O.quantize_with(w, n, k, fmt, "pcs", 1.0)
+
+    for n, k, unit in ((4096, 14336, False), (1000, 4096, False), (777, 1008, True), (96, 40000, False)):
+        q = quant(n, k)
+        codes, scales = dev(q.codes.reshape(-1)), None if unit else dev(q.scales)
+        x = dev(bf16_bits(rng.standard_normal(k).astype(np.float32)).view(np.int16))
+        res = dev(rng.standard_normal(n).astype(np.float32))
+        want = R.add_bf16_f32(res, R.gemm_w8a16(x, codes, scales, 1, n, k, fmt), n).cpu().numpy()
+        got = R.gemv_residual(x, codes, scales, n, k, fmt, res).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, k)
+        R.gemv_residual(x, codes, scales, n, k, fmt, res, out=res)   # in place
+        assert np.array_equal(res.cpu().numpy().view(np.uint32), want.view(np.uint32)), (n, k, "in place")
+    for inter, k, unit in ((14336, 4096, False), (1001, 1008, False), (300, 14336, True), (48, 40000, False)):
+        g, u = quant(inter, k), quant(inter, k)
+        x = dev(bf16_bits(rng.standard_normal(k).astype(np.float32)).view(np.int16))
+        sg = None if unit else dev(g.scales)
+        su = None if unit else dev(u.scales)
+        gy = R.gemm_w8a16(x, dev(g.codes.reshape(-1)), sg, 1, inter, k, fmt)
+        uy = R.gemm_w8a16(x, dev(u.codes.reshape(-1)), su, 1, inter, k, fmt)
+        want = bits(R.silu_mul_bf16(gy, uy, inter))
+        pc = np.empty((2 * inter, k), dtype=np.uint8)
+        pc[0::2], pc[1::2] = g.codes.reshape(inter, k), u.codes.reshape(inter, k)
+        ps = np.empty(2 * inter, dtype=np.float32)
+        ps[0::2], ps[1::2] = g.scales, u.scales
+        got = bits(R.gemv_swiglu(x, dev(pc.reshape(-1)), None if unit else dev(ps), 2 * inter, k, fmt))
+        assert np.array_equal(got, want), (inter, k)
 
 
 def _attention_want(Q, K, V, nh, nkv, hd, scale):
