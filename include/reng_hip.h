@@ -203,6 +203,22 @@ RENG_HIP_API int reng_hip_gemv_w8a16_residual(const uint16_t *x, const uint8_t *
 RENG_HIP_API int reng_hip_gemv_w8a16_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales,
                                             size_t N, size_t K, int format, uint16_t *y, void *stream);
 
+/* reng_hip_gemm_w8a16 at M = 1 with the RMSNorm of its input as its prologue:
+ * y = bf16(W . bf16(rms_norm(x) * gamma)), x and gamma f32 [K] (4-byte
+ * aligned), K % 16 == 0, K <= 32768; every workgroup normalises the row
+ * itself. Bit-identical to reng_hip_rms_norm_bf16 (one row) then
+ * reng_hip_gemm_w8a16. */
+RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm(const float *x, const float *gamma, float eps, const uint8_t *codes,
+                                             const float *scales, size_t N, size_t K, int format, uint16_t *y,
+                                             void *stream);
+
+/* The same prologue with reng_hip_gemv_w8a16_swiglu's epilogue (rows in (gate,
+ * up) pairs, y bf16 [N / 2]): a SwiGLU MLP's norm, gate, up and activation in
+ * one pass. */
+RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm_swiglu(const float *x, const float *gamma, float eps,
+                                                    const uint8_t *codes, const float *scales, size_t N, size_t K,
+                                                    int format, uint16_t *y, void *stream);
+
 /* h = x + d and out = bf16(rms_norm(h) * gamma) in one pass, x and h f32, d
  * bf16 [rows, cols] (a branch output added to the residual stream, then the
  * next sublayer's RMSNorm; h must not overlap x or d). */

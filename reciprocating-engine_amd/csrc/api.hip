@@ -329,6 +329,40 @@ RENG_HIP_API int reng_hip_gemv_w8a16_swiglu(const uint16_t *x, const uint8_t *co
     return launch_gemv_swiglu(x, codes, scales, (uint32_t)N, (uint32_t)K, format, y, as_stream(stream));
 }
 
+namespace {
+
+int gemv_norm(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales, size_t N,
+              size_t K, int format, bool swiglu, uint16_t *y, void *stream) {
+    clear_error();
+    RENG_REQUIRE(valid_format(format), "unknown fp8 format %d", format);
+    RENG_REQUIRE(N > 0 && K > 0, "empty product 1 x %zu x %zu", N, K);
+    RENG_REQUIRE(K % 16 == 0, "K = %zu is not a multiple of 16", K);
+    RENG_REQUIRE(K <= 32768, "K = %zu is past 32768 (the normalised row is staged in 64 KB of LDS)", K);
+    RENG_REQUIRE(N <= 0x7fffffff, "dimension too large");
+    RENG_REQUIRE(!swiglu || N % 2 == 0, "N = %zu rows do not form (gate, up) pairs", N);
+    RENG_REQUIRE(eps >= 0.0f, "eps %g is negative", (double)eps);
+    RENG_REQUIRE(x && gamma && codes && y, "null pointer");
+    RENG_REQUIRE((reinterpret_cast<uintptr_t>(codes) & 15) == 0, "codes must be 16-byte aligned");
+    RENG_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma)) & 3) == 0,
+                 "x and gamma must be 4-byte aligned");
+    return launch_gemv_norm(x, gamma, eps, codes, scales, (uint32_t)N, (uint32_t)K, format, swiglu, y,
+                            as_stream(stream));
+}
+
+}  // namespace
+
+RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm(const float *x, const float *gamma, float eps, const uint8_t *codes,
+                                             const float *scales, size_t N, size_t K, int format, uint16_t *y,
+                                             void *stream) {
+    return gemv_norm(x, gamma, eps, codes, scales, N, K, format, false, y, stream);
+}
+
+RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm_swiglu(const float *x, const float *gamma, float eps,
+                                                    const uint8_t *codes, const float *scales, size_t N, size_t K,
+                                                    int format, uint16_t *y, void *stream) {
+    return gemv_norm(x, gamma, eps, codes, scales, N, K, format, true, y, stream);
+}
+
 RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const float *scale_a,
                                           size_t n_scale_a, const uint8_t *b, int b_format,
                                           const float *scale_b, size_t n_scale_b, size_t M,

@@ -231,6 +231,61 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
+// ---------------------------------------------------------------- RMSNorm
+
+// 1 / sqrt(mean(h^2) + eps) of a row h[0, cols) (rms_norm_cpu,
+// crates/reng-synapse/src/ops.rs:49-72), summed the way a 1024-thread
+// workgroup sums it: thread t takes columns 4t, 4t + 4096, ... (VEC: float4
+// loads; cols % 4 == 0, xr 16-byte aligned) or t, t + 1024, ...; each wave's
+// partial sums meet in wave_sum_dpp; the 16 wave sums are added in order. A
+// workgroup of 1024 / NV threads gets the same bits, each thread standing for
+// NV of those 1024. With ADD the row is h = x + bf16 d, written to hr as it is
+// formed; otherwise h = x. Every thread gets the result. red: 16 floats of LDS.
+constexpr int NORM_VT = 1024;
+
+template <bool VEC, bool ADD, int NV>
+__device__ __forceinline__ float row_inv_rms(const float *__restrict__ xr, const uint16_t *__restrict__ dr,
+                                             float *__restrict__ hr, uint32_t cols, float eps, float *red) {
+    const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t vt = threadIdx.x + i * (NORM_VT / NV);
+        float ss = 0.0f;
+        if constexpr (VEC) {
+            for (uint32_t c = vt * 4; c < cols; c += NORM_VT * 4) {
+                float4 v = *reinterpret_cast<const float4 *>(xr + c);
+                if constexpr (ADD) {
+                    const uint32_t w0 = *reinterpret_cast<const uint32_t *>(dr + c);
+                    const uint32_t w1 = *reinterpret_cast<const uint32_t *>(dr + c + 2);
+                    v.x += __uint_as_float(w0 << 16);
+                    v.y += __uint_as_float(w0 & 0xffff0000u);
+                    v.z += __uint_as_float(w1 << 16);
+                    v.w += __uint_as_float(w1 & 0xffff0000u);
+                    *reinterpret_cast<float4 *>(hr + c) = v;
+                }
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        } else {
+            for (uint32_t c = vt; c < cols; c += NORM_VT) {
+                float v = xr[c];
+                if constexpr (ADD) {
+                    v += __uint_as_float((uint32_t)dr[c] << 16);
+                    hr[c] = v;
+                }
+                ss += v * v;
+            }
+        }
+        ss = wave_sum_dpp(ss);
+        if (lane == 0) red[vt >> 6] = ss;
+    }
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NORM_VT / 64; ++w) s += red[w];
+    const float ms = s / (float)cols;
+    return 1.0f / sqrtf(ms + eps);
+}
+
 // bf16 bits (RNE, NaN -> 0x7fc0) of an f32 (lib.rs:41-48).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
     const uint32_t bits = __float_as_uint(x);

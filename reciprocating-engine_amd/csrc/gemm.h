@@ -15,6 +15,10 @@ int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *s
                          int format, const float *res, float *y, hipStream_t st);
 int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                        int format, uint16_t *y, hipStream_t st);
+// M = 1 with an RMSNorm prologue: the activation is bf16(rms_norm(x) * gamma), x f32 [K], K <= 32768; the
+// plain or the SwiGLU-pair epilogue.
+int launch_gemv_norm(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
+                     uint32_t N, uint32_t K, int format, bool swiglu, uint16_t *y, hipStream_t st);
 // 4 < M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st);

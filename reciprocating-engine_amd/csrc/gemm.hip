@@ -2,7 +2,8 @@
 //
 // 1. gemv_w8a16     (M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
 //                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]); with
-//                    M = 1 also a residual-add epilogue and a SwiGLU-pair one.
+//                    M = 1 also a residual-add epilogue, a SwiGLU-pair one and
+//                    an RMSNorm prologue.
 //    Streams the codes once with 16-byte loads, decodes in registers
 //    (v_cvt_pk_f32_fp8 / _bf8), f32 FMA, one wave per output row.
 // 2. The other M <= 64: the same product on bf16 MFMA with the codes and the
@@ -100,15 +101,25 @@ __device__ __forceinline__ uint16_t silu_mul_bits(uint32_t g, uint32_t u) {
     return (uint16_t)f32_to_bf16_bits(gv / (1.0f + expf(-gv)) * uv);
 }
 
-template <int F, int M, int CPL, bool XLDS, bool RAGGED, int EPI = EPI_PLAIN>
+//
+// Prologue PRO_NORM (M = 1, XLDS): x is an f32 row h [K] and the row staged is
+// bf16(h * inv * gamma), its RMSNorm, inv formed as row_inv_rms forms it in a
+// 1024-thread workgroup (so the staged row is rms_norm_rows' output, bit for
+// bit); PRO_NORM_VEC takes h four columns at a time (K % 4 == 0, h and gamma
+// 16-byte aligned), as rms_norm_rows' VEC form does.
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_NORM_VEC = 2 };
+
+template <int F, int M, int CPL, bool XLDS, bool RAGGED, int EPI = EPI_PLAIN, int PRO = PRO_NONE>
 __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x,
                                                   const uint8_t *__restrict__ codes,
                                                   const float *__restrict__ scales, uint32_t N,
                                                   uint32_t K, uint16_t *__restrict__ y, const float *res,
-                                                  float *yres) {
+                                                  float *yres, const float *__restrict__ gamma, float eps) {
     static_assert(EPI == EPI_PLAIN || M == 1, "the fused epilogues take one activation row");
+    static_assert(PRO == PRO_NONE || (M == 1 && XLDS), "the RMSNorm prologue stages one row in LDS");
     constexpr bool PAIRS = EPI == EPI_SWIGLU;
     extern __shared__ __attribute__((aligned(16))) uint32_t xs[];
+    __shared__ float red[PRO == PRO_NONE ? 1 : NORM_VT / 64];
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t nch = K / 16;   // 16-code chunks per row
     const uint32_t waves = gridDim.x * (blockDim.x >> 6);
@@ -151,7 +162,23 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
         load(r, gi, qn);
         if (scales) scales_from(0);
     }
-    if constexpr (XLDS) {
+    if constexpr (PRO != PRO_NONE) {
+        const float *xf = reinterpret_cast<const float *>(x);
+        const float inv = row_inv_rms<PRO == PRO_NORM_VEC, false, NORM_VT / 512>(xf, nullptr, nullptr, K, eps, red);
+        uint16_t *dst = reinterpret_cast<uint16_t *>(xs);
+        if constexpr (PRO == PRO_NORM_VEC) {
+            for (uint32_t c = tid * 4; c < K; c += 512 * 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(xf + c);
+                const float4 gv = *reinterpret_cast<const float4 *>(gamma + c);
+                const uint32_t lo = f32_to_bf16_bits(v.x * inv * gv.x) | (f32_to_bf16_bits(v.y * inv * gv.y) << 16);
+                const uint32_t hi = f32_to_bf16_bits(v.z * inv * gv.z) | (f32_to_bf16_bits(v.w * inv * gv.w) << 16);
+                *reinterpret_cast<u32x2 *>(dst + c) = u32x2{lo, hi};
+            }
+        } else {
+            for (uint32_t c = tid; c < K; c += 512) dst[c] = (uint16_t)f32_to_bf16_bits(xf[c] * inv * gamma[c]);
+        }
+        __syncthreads();
+    } else if constexpr (XLDS) {
         const u32x4 *src = reinterpret_cast<const u32x4 *>(x);
         u32x4 *dst = reinterpret_cast<u32x4 *>(xs);
         for (uint32_t i = tid; i < M * nch * 2; i += blockDim.x) dst[i] = src[i];
@@ -302,35 +329,68 @@ GemvPlan gemv_plan(uint32_t M, uint32_t N, uint32_t K, uint32_t unit) {
     return p;
 }
 
-template <int F, int EPI>
+template <int F, int EPI, int PRO = PRO_NONE>
 int launch_gemv_epi_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
-                      uint16_t *y, const float *res, float *yres, hipStream_t st) {
+                      uint16_t *y, const float *res, float *yres, const float *gamma, float eps, hipStream_t st) {
     const GemvPlan p = gemv_plan(1, N, K, EPI == EPI_SWIGLU ? 2 : 1);
+    if (PRO != PRO_NONE && !p.xlds) {
+        set_error("K = %u: the RMSNorm prologue stages the row in 64 KB of LDS (K <= 32768)", K);
+        return RENG_HIP_EINVAL;
+    }
 #define RENG_GEMV_E(C, XL, RG)                                                                                  \
-    hipLaunchKernelGGL((gemv_w8a16<F, 1, C, XL, RG, EPI>), dim3(p.blocks), dim3(GemvPlan::threads), p.lds, st, x, \
-                       codes, scales, N, K, y, res, yres)
+    hipLaunchKernelGGL((gemv_w8a16<F, 1, C, XL, RG, EPI, PRO>), dim3(p.blocks), dim3(GemvPlan::threads), p.lds, \
+                       st, x, codes, scales, N, K, y, res, yres, gamma, eps)
+    if constexpr (PRO != PRO_NONE) {
+        if (p.cpl7) RENG_GEMV_E(7, true, false);
+        else if (p.ragged) RENG_GEMV_E(4, true, true);
+        else RENG_GEMV_E(4, true, false);
+    } else {
 #define RENG_GEMV_EX(C, RG) \
     if (p.xlds) RENG_GEMV_E(C, true, RG); else RENG_GEMV_E(C, false, RG);
-    if (p.cpl7) { RENG_GEMV_EX(7, false) }
-    else if (p.ragged) { RENG_GEMV_EX(4, true) }
-    else { RENG_GEMV_EX(4, false) }
+        if (p.cpl7) { RENG_GEMV_EX(7, false) }
+        else if (p.ragged) { RENG_GEMV_EX(4, true) }
+        else { RENG_GEMV_EX(4, false) }
 #undef RENG_GEMV_EX
+    }
 #undef RENG_GEMV_E
-    return check_launch(EPI == EPI_SWIGLU ? "gemv_w8a16 (SwiGLU pairs)" : "gemv_w8a16 (residual)");
+    return check_launch(EPI == EPI_SWIGLU ? "gemv_w8a16 (SwiGLU pairs)"
+                        : EPI == EPI_RESID ? "gemv_w8a16 (residual)"
+                                           : "gemv_w8a16 (RMSNorm)");
+}
+
+template <int F, int EPI>
+int launch_gemv_norm_t(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
+                       uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
+    const uint16_t *xa = reinterpret_cast<const uint16_t *>(x);
+    const bool vec =
+        K % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma)) & 15) == 0;
+    return vec ? launch_gemv_epi_t<F, EPI, PRO_NORM_VEC>(xa, codes, scales, N, K, y, nullptr, nullptr, gamma, eps, st)
+               : launch_gemv_epi_t<F, EPI, PRO_NORM>(xa, codes, scales, N, K, y, nullptr, nullptr, gamma, eps, st);
+}
+
+int launch_gemv_norm(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
+                     uint32_t N, uint32_t K, int format, bool swiglu, uint16_t *y, hipStream_t st) {
+    if (format == RENG_HIP_E4M3)
+        return swiglu ? launch_gemv_norm_t<RENG_HIP_E4M3, EPI_SWIGLU>(x, gamma, eps, codes, scales, N, K, y, st)
+                      : launch_gemv_norm_t<RENG_HIP_E4M3, EPI_PLAIN>(x, gamma, eps, codes, scales, N, K, y, st);
+    return swiglu ? launch_gemv_norm_t<RENG_HIP_E5M2, EPI_SWIGLU>(x, gamma, eps, codes, scales, N, K, y, st)
+                  : launch_gemv_norm_t<RENG_HIP_E5M2, EPI_PLAIN>(x, gamma, eps, codes, scales, N, K, y, st);
 }
 
 int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                          int format, const float *res, float *y, hipStream_t st) {
     return format == RENG_HIP_E4M3
-               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, st)
-               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, st);
+               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, nullptr, 0.0f, st)
+               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, nullptr, 0.0f, st);
 }
 
 int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                        int format, uint16_t *y, hipStream_t st) {
     return format == RENG_HIP_E4M3
-               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_SWIGLU>(x, codes, scales, N, K, y, nullptr, nullptr, st)
-               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_SWIGLU>(x, codes, scales, N, K, y, nullptr, nullptr, st);
+               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_SWIGLU>(x, codes, scales, N, K, y, nullptr, nullptr, nullptr,
+                                                              0.0f, st)
+               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_SWIGLU>(x, codes, scales, N, K, y, nullptr, nullptr, nullptr,
+                                                              0.0f, st);
 }
 
 template <int F>
@@ -361,7 +421,7 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
         const bool xlds = p.xlds, cpl7 = p.cpl7, ragged = p.ragged;
 #define RENG_GEMV(MM, C, XL, RG)                                                                   \
     hipLaunchKernelGGL((gemv_w8a16<F, MM, C, XL, RG>), dim3(blocks), dim3(threads), lds, st, x, codes, \
-                       scales, N, K, y, nullptr, nullptr)
+                       scales, N, K, y, nullptr, nullptr, nullptr, 0.0f)
 #define RENG_GEMV_X(MM, C, RG) \
     if (xlds) RENG_GEMV(MM, C, true, RG); else RENG_GEMV(MM, C, false, RG);
 #define RENG_GEMV_M(MM)                                  \

@@ -53,54 +53,26 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return m;
 }
 
-// out[r, c] = bf16(x[r, c] * inv_r * g[c]), inv_r = 1 / sqrt(mean_c x[r, c]^2 + eps)
-// (rms_norm_cpu, ops.rs:49-72). With ADD the row normalised is h = x + d (d a
-// bf16 branch output), which is also written out. One 1024-thread workgroup
-// per row; VEC moves four columns per thread and access (cols % 4 == 0,
-// aligned rows), so a row of up to 4096 columns is one load per thread.
-constexpr int NORM_THREADS = 1024;
-
+// out[r, c] = bf16(h[r, c] * inv_r * g[c]), inv_r = 1 / sqrt(mean_c h[r, c]^2 +
+// eps) (rms_norm_cpu, ops.rs:49-72), h = x, or with ADD h = x + d (d a bf16
+// branch output), which is also written out. One 1024-thread workgroup per
+// row (row_inv_rms); VEC moves four columns per thread and access (cols % 4
+// == 0, aligned rows), so a row of up to 4096 columns is one load per thread.
 template <bool VEC, bool ADD>
-__global__ __launch_bounds__(NORM_THREADS) void rms_norm_rows(const float *__restrict__ x,
-                                                              const uint16_t *__restrict__ d,
-                                                              const float *__restrict__ g, uint32_t cols, float eps,
-                                                              float *__restrict__ h, uint16_t *__restrict__ out) {
-    __shared__ float red[NORM_THREADS / 64];
+__global__ __launch_bounds__(NORM_VT) void rms_norm_rows(const float *__restrict__ x,
+                                                         const uint16_t *__restrict__ d,
+                                                         const float *__restrict__ g, uint32_t cols, float eps,
+                                                         float *__restrict__ h, uint16_t *__restrict__ out) {
+    __shared__ float red[NORM_VT / 64];
     const size_t base = (size_t)blockIdx.x * cols;
     const float *xr = x + base;
     float *hr = ADD ? h + base : nullptr;
-    const uint16_t *dr = ADD ? d + base : nullptr;
     uint16_t *orow = out + base;
-    float ss = 0.0f;
-    if constexpr (VEC) {
-        for (uint32_t c = threadIdx.x * 4; c < cols; c += NORM_THREADS * 4) {
-            float4 v = *reinterpret_cast<const float4 *>(xr + c);
-            if constexpr (ADD) {
-                const u32x2 w = *reinterpret_cast<const u32x2 *>(dr + c);
-                v.x += __uint_as_float(w.x << 16);
-                v.y += __uint_as_float(w.x & 0xffff0000u);
-                v.z += __uint_as_float(w.y << 16);
-                v.w += __uint_as_float(w.y & 0xffff0000u);
-                *reinterpret_cast<float4 *>(hr + c) = v;
-            }
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-    } else {
-        for (uint32_t c = threadIdx.x; c < cols; c += NORM_THREADS) {
-            float v = xr[c];
-            if constexpr (ADD) {
-                v += bf16_f32(dr[c]);
-                hr[c] = v;
-            }
-            ss += v * v;
-        }
-    }
-    const float ms = block_sum(ss, red) / (float)cols;
-    const float inv = 1.0f / sqrtf(ms + eps);
+    const float inv = row_inv_rms<VEC, ADD, 1>(xr, ADD ? d + base : nullptr, hr, cols, eps, red);
     // The second pass reads back what this thread read (or wrote) in the first.
     const float *src = ADD ? hr : xr;
     if constexpr (VEC) {
-        for (uint32_t c = threadIdx.x * 4; c < cols; c += NORM_THREADS * 4) {
+        for (uint32_t c = threadIdx.x * 4; c < cols; c += NORM_VT * 4) {
             const float4 v = *reinterpret_cast<const float4 *>(src + c);
             const float4 gv = *reinterpret_cast<const float4 *>(g + c);
             const uint32_t lo = f32_bf16(v.x * inv * gv.x) | ((uint32_t)f32_bf16(v.y * inv * gv.y) << 16);
@@ -108,7 +80,7 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_rows(const float *__res
             *reinterpret_cast<u32x2 *>(orow + c) = u32x2{lo, hi};
         }
     } else {
-        for (uint32_t c = threadIdx.x; c < cols; c += NORM_THREADS) orow[c] = f32_bf16(src[c] * inv * g[c]);
+        for (uint32_t c = threadIdx.x; c < cols; c += NORM_VT) orow[c] = f32_bf16(src[c] * inv * g[c]);
     }
 }
 
@@ -159,6 +131,7 @@ __global__ __launch_bounds__(64) void rope_append(uint16_t *__restrict__ q, cons
 // writes bf16(o / l); otherwise it writes the unnormalised o and (m, l) of its
 // split to the workspace and attention_combine merges the splits.
 constexpr int ATT_THREADS = 256, ATT_TILE = 64, ATT_GMAX = 8, ATT_SPLIT_MAX = 64, ATT_SPLIT_ROWS = 32;
+constexpr int ATT_VPF = 16;   // value rows per thread requested with the tile's keys
 
 struct AttnPlan {
     uint32_t splits, chunk;
@@ -223,6 +196,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
     const uint32_t l16 = lane & 15, rg = lane >> 4;
     for (uint32_t t0 = j0; t0 < j1; t0 += ATT_TILE) {
         const uint32_t n = min((uint32_t)ATT_TILE, j1 - t0);
+        // Phase 2's first ATT_VPF value rows (first pair) are requested before
+        // phase 1's keys, so the two memory round trips overlap.
+        uint32_t vpf[ATT_VPF];
+#pragma unroll
+        for (int i = 0; i < ATT_VPF; ++i) {
+            const uint32_t jj = ph + i * nph;
+            vpf[i] = active && jj < n
+                         ? *reinterpret_cast<const uint32_t *>(vbase + (size_t)(t0 + jj) * pitch + 2 * dp)
+                         : 0u;
+        }
         // Phase 1: rows wave * 16 + it * 4 + rg of the tile.
         float acc[4][ATT_GMAX];
 #pragma unroll
@@ -315,9 +298,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
                 }
             }
             const bool two = dp + ATT_THREADS < npairs;
-            for (uint32_t jj = ph; jj < n; jj += nph) {
+            auto accumulate = [&](uint32_t jj, uint32_t w0) {
                 const uint16_t *vr = vbase + (size_t)(t0 + jj) * pitch;
-                const uint32_t w0 = *reinterpret_cast<const uint32_t *>(vr + 2 * dp);
                 const uint32_t w1 = two ? *reinterpret_cast<const uint32_t *>(vr + 2 * (dp + ATT_THREADS)) : 0u;
                 const float a0 = __uint_as_float(w0 << 16), a1 = __uint_as_float(w0 & 0xffff0000u);
                 const float b0 = __uint_as_float(w1 << 16), b1 = __uint_as_float(w1 & 0xffff0000u);
@@ -330,7 +312,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
                     o[h][1][0] += p * b0;
                     o[h][1][1] += p * b1;
                 }
+            };
+#pragma unroll
+            for (int i = 0; i < ATT_VPF; ++i) {
+                const uint32_t jj = ph + i * nph;
+                if (jj < n) accumulate(jj, vpf[i]);
             }
+            for (uint32_t jj = ph + ATT_VPF * nph; jj < n; jj += nph)
+                accumulate(jj, *reinterpret_cast<const uint32_t *>(vbase + (size_t)(t0 + jj) * pitch + 2 * dp));
         }
         __syncthreads();
     }
@@ -385,6 +374,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_combine(const float *__
     __syncthreads();
     for (uint32_t d = tid; d < hd; d += ATT_THREADS) {
         float v = 0.0f;
+#pragma unroll 16
         for (uint32_t i = 0; i < splits; ++i) v += wsp[i] * part[((size_t)i * nh + h) * hd + d];
         out[(size_t)h * hd + d] = f32_bf16(v);
     }
@@ -434,10 +424,10 @@ int launch_norm(const float *x, const uint16_t *d, const float *gamma, size_t ro
     const uintptr_t a8 = reinterpret_cast<uintptr_t>(d) | reinterpret_cast<uintptr_t>(out);
     const bool vec = cols % 4 == 0 && (a16 & 15) == 0 && (a8 & 7) == 0;
     if (vec)
-        hipLaunchKernelGGL((rms_norm_rows<true, ADD>), dim3((unsigned)rows), dim3(NORM_THREADS), 0, st, x, d, gamma,
+        hipLaunchKernelGGL((rms_norm_rows<true, ADD>), dim3((unsigned)rows), dim3(NORM_VT), 0, st, x, d, gamma,
                            (uint32_t)cols, eps, h, out);
     else
-        hipLaunchKernelGGL((rms_norm_rows<false, ADD>), dim3((unsigned)rows), dim3(NORM_THREADS), 0, st, x, d, gamma,
+        hipLaunchKernelGGL((rms_norm_rows<false, ADD>), dim3((unsigned)rows), dim3(NORM_VT), 0, st, x, d, gamma,
                            (uint32_t)cols, eps, h, out);
     return check_launch("rms_norm_rows");
 }

@@ -49,6 +49,10 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
         throw Error("Fp8Decoder: max_positions " + std::to_string(max_pos_) + " is not in [1, " +
                     std::to_string(RENG_HIP_ATTENTION_MAX_LEN) + "]");
     if (w.fp8->size() != w.layers.size()) throw Error("Fp8Decoder: fp8 layers do not match the weights");
+    // The normalised row a GEMV reads is staged whole in its workgroups' LDS.
+    if (hidden_ > 32768)
+        throw Error("Fp8Decoder: hidden_size " + std::to_string(hidden_) + " is past 32768, which the fp8 decode step "
+                    "does not implement");
 
     auto dev = [&](size_t bytes) {
         void *p = nullptr;
@@ -146,12 +150,10 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
         x_ = static_cast<float *>(dev(hidden_ * 4));
         h_ = static_cast<float *>(dev(hidden_ * 4));
         // bf16 buffers 16-byte aligned (hipMalloc) for the GEMV's inputs.
-        n_ = static_cast<uint16_t *>(dev(hidden_ * 2));
         q_ = static_cast<uint16_t *>(dev((qd + 2 * kvd) * 2));   // q | k | v, one GEMV's output
         k_ = q_ + qd;
         v_ = k_ + kvd;
         a_ = static_cast<uint16_t *>(dev(qd * 2));
-        o_ = static_cast<uint16_t *>(dev(hidden_ * 2));
         act_ = static_cast<uint16_t *>(dev(inter_ * 2));
         attn_ws_bytes_ = reng_hip_attention_workspace_bytes(nh_, hd_, max_pos_);
         attn_ws_ = dev(attn_ws_bytes_);
@@ -167,10 +169,6 @@ Fp8Decoder::~Fp8Decoder() {
     for (void *p : allocs_) (void)hipFree(p);
 }
 
-void Fp8Decoder::gemv(const Mat &m, const uint16_t *x, uint16_t *y, void *stream) {
-    abi_ok(reng_hip_gemm_w8a16(x, m.codes, m.scales, 1, m.rows, m.cols, m.format, y, stream));
-}
-
 void Fp8Decoder::step_device(size_t li, const float *x, float *y, size_t pos, void *stream) {
     Layer &L = layers_.at(li);
     if (pos != L.pos)
@@ -178,16 +176,18 @@ void Fp8Decoder::step_device(size_t li, const float *x, float *y, size_t pos, vo
                     ", asked for " + std::to_string(pos));
     if (pos >= max_pos_) throw Error("Fp8Decoder: position " + std::to_string(pos) + " is past the cache");
     const size_t kvd = nkv_ * hd_;
-    abi_ok(reng_hip_rms_norm_bf16(x, L.g1, 1, hidden_, eps_, n_, stream));
-    gemv(L.wqkv, n_, q_, stream);
+    // Norm + q/k/v; RoPE and the cache append; attention; o-proj + residual
+    // (h); norm + gate/up + SiLU * up; down + residual (y).
+    abi_ok(reng_hip_gemv_w8a16_rmsnorm(x, L.g1, eps_, L.wqkv.codes, L.wqkv.scales, L.wqkv.rows, L.wqkv.cols,
+                                       L.wqkv.format, q_, stream));
     abi_ok(reng_hip_rope_append(q_, k_, v_, nh_, nkv_, hd_, sin_ + pos * hd_, cos_ + pos * hd_,
                                 L.kcache + pos * kvd, L.vcache + pos * kvd, stream));
     abi_ok(reng_hip_attention_decode_split(q_, L.kcache, L.vcache, nh_, nkv_, hd_, pos + 1, scale_, attn_ws_,
                                            attn_ws_bytes_, a_, stream));
-    gemv(L.wo, a_, o_, stream);
-    abi_ok(reng_hip_add_rms_norm_bf16(x, o_, L.g2, 1, hidden_, eps_, h_, n_, stream));
-    abi_ok(reng_hip_gemv_w8a16_swiglu(n_, L.wgu.codes, L.wgu.scales, L.wgu.rows, L.wgu.cols, L.wgu.format, act_,
-                                      stream));
+    abi_ok(reng_hip_gemv_w8a16_residual(a_, L.wo.codes, L.wo.scales, L.wo.rows, L.wo.cols, L.wo.format, x, h_,
+                                        stream));
+    abi_ok(reng_hip_gemv_w8a16_rmsnorm_swiglu(h_, L.g2, eps_, L.wgu.codes, L.wgu.scales, L.wgu.rows, L.wgu.cols,
+                                              L.wgu.format, act_, stream));
     abi_ok(reng_hip_gemv_w8a16_residual(act_, L.wd.codes, L.wd.scales, L.wd.rows, L.wd.cols, L.wd.format, h_, y,
                                         stream));
     ++L.pos;

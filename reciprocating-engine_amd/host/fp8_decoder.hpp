@@ -30,8 +30,8 @@ class Fp8Decoder {
     // for them. Throws Error when w.fp8 is empty, for a model this step does not
     // implement (a model_type other than llama / mistral, rope_scaling, a
     // sliding window, an attention scale override, head_dim odd), for
-    // max_positions outside [1, RENG_HIP_ATTENTION_MAX_LEN], and on a device
-    // failure.
+    // max_positions outside [1, RENG_HIP_ATTENTION_MAX_LEN], hidden_size past
+    // 32768, and on a device failure.
     Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max_positions);
     ~Fp8Decoder();
     Fp8Decoder(const Fp8Decoder &) = delete;
@@ -67,7 +67,6 @@ class Fp8Decoder {
         uint16_t *kcache = nullptr, *vcache = nullptr;
         size_t pos = 0;
     };
-    void gemv(const Mat &m, const uint16_t *x, uint16_t *y, void *stream);
 
     size_t hidden_, inter_, nh_, nkv_, hd_, max_pos_;
     float eps_, scale_;
@@ -76,7 +75,7 @@ class Fp8Decoder {
     float *sin_ = nullptr, *cos_ = nullptr;
     // scratch: residual f32 rows, bf16 GEMV inputs and outputs
     float *x_ = nullptr, *h_ = nullptr;
-    uint16_t *n_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *a_ = nullptr, *o_ = nullptr;
+    uint16_t *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *a_ = nullptr;
     uint16_t *act_ = nullptr;
     // the split attention's partial outputs (one layer at a time)
     void *attn_ws_ = nullptr;

@@ -63,6 +63,8 @@ SIGNATURES = {
     "reng_hip_add_rms_norm_bf16": (_I, [_P, _P, _P, _SZ, _SZ, _F, _P, _P, _P]),
     "reng_hip_gemv_w8a16_residual": (_I, [_P, _P, _P, _SZ, _SZ, _I, _P, _P, _P]),
     "reng_hip_gemv_w8a16_swiglu": (_I, [_P, _P, _P, _SZ, _SZ, _I, _P, _P]),
+    "reng_hip_gemv_w8a16_rmsnorm": (_I, [_P, _P, _F, _P, _P, _SZ, _SZ, _I, _P, _P]),
+    "reng_hip_gemv_w8a16_rmsnorm_swiglu": (_I, [_P, _P, _F, _P, _P, _SZ, _SZ, _I, _P, _P]),
     "reng_hip_rope_append": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P]),
     "reng_hip_attention_decode": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _P]),
     "reng_hip_attention_workspace_bytes": (_SZ, [_SZ, _SZ, _SZ]),
@@ -355,6 +357,19 @@ def gemv_swiglu(x, codes, scales, n, k, fmt, out=None):
     _check(lib().reng_hip_gemv_w8a16_swiglu(_dev(x, "x"), _dev(codes, "codes"),
                                             None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt),
                                             _dev(out, "out"), _stream()))
+    return out
+
+
+def gemv_rmsnorm(x, gamma, eps, codes, scales, n, k, fmt, swiglu=False, out=None):
+    """bf16 out = W . bf16(rms_norm(x) * gamma), x f32 [k]; with swiglu the rows
+    of codes alternate gate, up and out[n / 2] = silu(gate) * up."""
+    import torch
+
+    if out is None:
+        out = torch.empty(n // 2 if swiglu else n, dtype=torch.bfloat16, device=x.device)
+    fn = lib().reng_hip_gemv_w8a16_rmsnorm_swiglu if swiglu else lib().reng_hip_gemv_w8a16_rmsnorm
+    _check(fn(_dev(x, "x"), _dev(gamma, "gamma"), eps, _dev(codes, "codes"),
+              None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt), _dev(out, "out"), _stream()))
     return out
 
 

@@ -234,6 +234,13 @@ def test_decode_step_entry_points_refuse_bad_arguments():
     assert sw(p, p, p, 7, 64, R.E4M3, p, None) == R.EINVAL                               # odd N
     assert b"pairs" in lib.reng_hip_last_error()
     assert sw(p, p, p, 0, 64, R.E4M3, p, None) == R.EINVAL
+    nm, nms = lib.reng_hip_gemv_w8a16_rmsnorm, lib.reng_hip_gemv_w8a16_rmsnorm_swiglu
+    assert nm(p, p, 1e-5, p, p, 8, 32784, R.E4M3, p, None) == R.EINVAL                  # past the LDS stage
+    assert b"32768" in lib.reng_hip_last_error()
+    assert nm(p, p, -1.0, p, p, 8, 64, R.E4M3, p, None) == R.EINVAL                     # eps
+    assert nm(ctypes.c_void_p(18), p, 1e-5, p, p, 8, 64, R.E4M3, p, None) == R.EINVAL   # x not 4-byte aligned
+    assert nm(p, None, 1e-5, p, p, 8, 64, R.E4M3, p, None) == R.EINVAL                  # no gamma
+    assert nms(p, p, 1e-5, p, p, 7, 64, R.E4M3, p, None) == R.EINVAL                    # odd N
     assert lib.reng_hip_add_bf16_f32(p, None, 4, p, None) == R.EINVAL
 
 
@@ -350,6 +357,41 @@ def test_gemv_epilogues_equal_the_unfused_steps(fmt):
         ps[0::2], ps[1::2] = g.scales, u.scales
         got = bits(R.gemv_swiglu(x, dev(pc.reshape(-1)), None if unit else dev(ps), 2 * inter, k, fmt))
         assert np.array_equal(got, want), (inter, k)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_gemv_rmsnorm_prologue_equals_norm_then_gemv(fmt):
+    """The RMSNorm prologue against rms_norm_bf16 then gemm_w8a16 (and then the
+    SwiGLU pairs against rms_norm_bf16 then gemv_swiglu), bit for bit: the
+    four-column form (K = 4096: one float4 per virtual thread; K = 14336:
+    several) and the one-column form (a row 4 bytes off a 16-byte boundary,
+    and K = 1008 with a gamma off its boundary)."""
+    import torch
+
+    import reng_hip as R
+
+    rng = np.random.default_rng(7 if fmt == "e4m3" else 8)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    for n, k, shift in ((6144, 4096, 0), (512, 14336, 0), (300, 4096, 1), (1000, 1008, 0), (96, 32768, 0)):
+        w = bf16_bits(rng.standard_normal((n, k)).astype(np.float32) * 0.05)
+        q = O.quantize_with(w, n, k, fmt, "pcs", 1.0)
+        codes, scales = dev(q.codes.reshape(-1)), dev(q.scales)
+        xb = torch.zeros(k + 4, dtype=torch.float32, device="cuda")
+        xb[shift:shift + k] = dev(rng.standard_normal(k).astype(np.float32) * 3)
+        x = xb[shift:shift + k]
+        gb = torch.zeros(k + 4, dtype=torch.float32, device="cuda")
+        gshift = 1 if k == 1008 else 0
+        gb[gshift:gshift + k] = dev((1 + rng.standard_normal(k) * 0.1).astype(np.float32))
+        g = gb[gshift:gshift + k]
+        normed = R.rms_norm_bf16(x, g, 1, k, 1e-5)
+        want = bits(R.gemm_w8a16(normed, codes, scales, 1, n, k, fmt))
+        got = bits(R.gemv_rmsnorm(x, g, 1e-5, codes, scales, n, k, fmt))
+        assert np.array_equal(got, want), (n, k, shift)
+        want = bits(R.gemv_swiglu(normed, codes, scales, n, k, fmt))
+        got = bits(R.gemv_rmsnorm(x, g, 1e-5, codes, scales, n, k, fmt, swiglu=True))
+        assert np.array_equal(got, want), (n, k, shift, "swiglu")
 
 
 def _attention_want(Q, K, V, nh, nkv, hd, scale):
