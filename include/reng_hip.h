@@ -236,24 +236,24 @@ RENG_HIP_API int reng_hip_rope_append(uint16_t *q, const uint16_t *k, const uint
 /* One query per head over cache rows 0 .. len - 1 (layer_cpu's causal attention,
  * model.rs:3010-3050): out[h] = softmax(scale * q[h] . K[:, g]) V[:, g] with
  * g = h / (n_heads / n_kv_heads), bf16 in and out, f32 inside (online softmax
- * over tiles of 64 rows); 1 <= len <= RENG_HIP_ATTENTION_MAX_LEN; k_cache and
- * v_cache 4-byte aligned. One workgroup per query head reads the whole cache:
- * for long caches use reng_hip_attention_decode_split. */
+ * over tiles of 256 rows); 1 <= len <= RENG_HIP_ATTENTION_MAX_LEN; q, k_cache
+ * and v_cache 4-byte aligned. One workgroup per query head reads the whole
+ * cache: for caches past 512 rows use reng_hip_attention_decode_split. */
 RENG_HIP_API int reng_hip_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                                            size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t len,
                                            float scale, uint16_t *out, void *stream);
 
 /* Bytes of device workspace reng_hip_attention_decode_split needs for every
- * cache length from 1 to len (0 when one split covers them all: len <= 32). */
+ * cache length from 1 to len (0 when all of them take one pass: len <= 512). */
 RENG_HIP_API size_t reng_hip_attention_workspace_bytes(size_t n_heads, size_t head_dim, size_t len);
 
-/* reng_hip_attention_decode with the cache cut into up to 64 splits of at
- * least 32 rows, one workgroup per split and group of query heads sharing a
- * key/value head (each split's rows read once for the group); the splits'
- * unnormalised outputs and softmax statistics go to workspace (f32, 4-byte
- * aligned, workspace_bytes >= reng_hip_attention_workspace_bytes(n_heads,
- * head_dim, len)) and a second kernel merges them. Asynchronous on stream;
- * calls that share a workspace must be ordered (one stream). */
+/* reng_hip_attention_decode that, past 512 cache rows, cuts the cache into
+ * min(64, ceil(len / 256)) splits, one workgroup per split and group of query
+ * heads sharing a key/value head (each split's rows read once for the group);
+ * the splits' unnormalised outputs and softmax statistics go to workspace
+ * (f32, 4-byte aligned, workspace_bytes >= reng_hip_attention_workspace_bytes(
+ * n_heads, head_dim, len)) and a second kernel merges them. Asynchronous on
+ * stream; calls that share a workspace must be ordered (one stream). */
 RENG_HIP_API int reng_hip_attention_decode_split(const uint16_t *q, const uint16_t *k_cache,
                                                  const uint16_t *v_cache, size_t n_heads, size_t n_kv_heads,
                                                  size_t head_dim, size_t len, float scale, void *workspace,

@@ -121,26 +121,37 @@ __global__ __launch_bounds__(64) void rope_append(uint16_t *__restrict__ q, cons
 // p = softmax(s), out_h = sum_j p_j v_j[g], with g = h / (nh / nkv).
 //
 // The cache is cut into S splits of `chunk` rows; workgroup (s, y) reads the
-// key and value rows of split s once for a group of gb query heads that share
-// key/value head g (gb divides nh / nkv, at most ATT_GMAX), 64 rows at a time
-// with an online softmax: per tile, phase 1 puts the tile's scores in LDS
-// (16 lanes per key row, 16-byte loads when head_dim % 8 == 0), the tile's
-// max and sum update the running (m, l) per head, and phase 2 accumulates
-// exp(s_j - m) v_j into registers (a thread per value-row dimension pair and
-// row phase, so each wave load is whole rows). With S = 1 the workgroup
-// writes bf16(o / l); otherwise it writes the unnormalised o and (m, l) of its
-// split to the workspace and attention_combine merges the splits.
-constexpr int ATT_THREADS = 256, ATT_TILE = 64, ATT_GMAX = 8, ATT_SPLIT_MAX = 64, ATT_SPLIT_ROWS = 32;
+// key and value rows of split s once for gb query heads that share
+// key/value head g (gb divides nh / nkv, at most ATT_GMAX), 256 rows at a time
+// with an online softmax. Per tile: the first ATT_VPF value rows of each
+// thread, the keys and the thread's slice of q are requested together (one
+// memory round trip); phase 1 forms the scores (16 lanes per key row, bf16
+// pairs into v_dot2_f32_bf16, 16-byte loads when head_dim % 8 == 0) into LDS;
+// the tile's max and sum update the running (m, l) per head; phase 2
+// accumulates exp(s_j - m) v_j in registers (a thread per value dimension pair
+// and row phase, so a wave's load is whole rows). With S = 1 the workgroup
+// writes bf16(o / l); otherwise the unnormalised o and (m, l) of its split go
+// to the workspace and attention_combine merges the splits.
+constexpr int ATT_NW = 16, ATT_THREADS = 64 * ATT_NW, ATT_TILE = 16 * ATT_NW, ATT_GMAX = 4;
+constexpr int ATT_SPLIT_MAX = 64, ATT_SPLIT_ROWS = 256, ATT_ONE_PASS_MAX = 512;
 constexpr int ATT_VPF = 16;   // value rows per thread requested with the tile's keys
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                           false);
+}
 
 struct AttnPlan {
     uint32_t splits, chunk;
 };
 
-// S = min(64, ceil(len / 32)) splits of equal length (the last one shorter),
+// One pass (S = 1) for caches of up to 512 rows or without a workspace; else
+// S = min(64, ceil(len / 256)) splits of equal length (the last one shorter),
 // none empty.
 inline AttnPlan attn_plan(size_t len, bool split) {
-    if (!split) return {1u, (uint32_t)len};
+    if (!split || len <= (size_t)ATT_ONE_PASS_MAX) return {1u, (uint32_t)len};
     size_t s = (len + ATT_SPLIT_ROWS - 1) / ATT_SPLIT_ROWS;
     if (s > (size_t)ATT_SPLIT_MAX) s = ATT_SPLIT_MAX;
     const size_t chunk = (len + s - 1) / s;
@@ -167,37 +178,35 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, uint32_t nh,
     uint32_t nkv, uint32_t hd, uint32_t len, uint32_t chunk, uint32_t gb, float scale, float *__restrict__ part,
     uint16_t *__restrict__ out) {
-    extern __shared__ float smem[];   // q [gb][hd] f32; after the tiles, o [nph][gb][hd]
+    extern __shared__ float op[];   // [nph][gb][hd]: the row phases' o, summed at the end
     __shared__ float sc[ATT_GMAX][ATT_TILE];
     __shared__ float mrun[ATT_GMAX], lrun[ATT_GMAX], corr[ATT_GMAX];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t s = blockIdx.x, h0 = blockIdx.y * gb, g = h0 / (nh / nkv);
+    const uint32_t per_kv = nh / nkv, s = blockIdx.x;
+    // One head per workgroup: y walks the key/value heads fastest, so the query
+    // heads of one key/value head sit gridDim.x * nkv blocks apart (on one XCD
+    // when that is a multiple of 8) and share its rows in L2.
+    const uint32_t h0 = gb == 1 ? (blockIdx.y % nkv) * per_kv + blockIdx.y / nkv : blockIdx.y * gb;
+    const uint32_t g = h0 / per_kv;
     const size_t pitch = (size_t)nkv * hd;
     const uint32_t j0 = s * chunk, j1 = min(len, j0 + chunk);
-    const uint16_t *kbase = kc + (size_t)g * hd, *vbase = vc + (size_t)g * hd;
-    float *qs = smem;
-    for (uint32_t i = tid; i < gb * hd; i += ATT_THREADS) qs[i] = bf16_f32(q[(size_t)h0 * hd + i]);
+    const uint16_t *kbase = kc + (size_t)g * hd, *vbase = vc + (size_t)g * hd, *qbase = q + (size_t)h0 * hd;
     if (tid < ATT_GMAX) {
         mrun[tid] = -INFINITY;
         lrun[tid] = 0.0f;
     }
-    // Phase 2 mapping: dimension pair dp (and dp + 256 when head_dim > 512) of
-    // the rows ph, ph + nph, ... of a tile.
+    // Phase 2: dimension pair dp of the tile rows ph, ph + nph, ...
     const uint32_t npairs = hd / 2, dpb = npairs < ATT_THREADS ? npairs : ATT_THREADS, nph = ATT_THREADS / dpb;
     const uint32_t ph = tid / dpb, dp = tid % dpb;
     const bool active = ph < nph;
-    float o[ATT_GMAX][2][2];
+    float o[ATT_GMAX][2];
 #pragma unroll
-    for (int h = 0; h < ATT_GMAX; ++h)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) o[h][e][0] = o[h][e][1] = 0.0f;
+    for (int h = 0; h < ATT_GMAX; ++h) o[h][0] = o[h][1] = 0.0f;
     __syncthreads();
 
     const uint32_t l16 = lane & 15, rg = lane >> 4;
     for (uint32_t t0 = j0; t0 < j1; t0 += ATT_TILE) {
         const uint32_t n = min((uint32_t)ATT_TILE, j1 - t0);
-        // Phase 2's first ATT_VPF value rows (first pair) are requested before
-        // phase 1's keys, so the two memory round trips overlap.
         uint32_t vpf[ATT_VPF];
 #pragma unroll
         for (int i = 0; i < ATT_VPF; ++i) {
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
         if constexpr (V8) {
             const uint32_t npc = hd / 8;
             for (uint32_t pc = l16; pc < npc; pc += 16) {
-                uint4 kv[4];
+                uint4 kv[4], qv[ATT_GMAX];
 #pragma unroll
                 for (int it = 0; it < 4; ++it) {
                     const uint32_t jj = wave * 16 + it * 4 + rg;
@@ -223,18 +232,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
                                     : uint4{0u, 0u, 0u, 0u};
                 }
 #pragma unroll
+                for (int h = 0; h < ATT_GMAX; ++h)
+                    qv[h] = h < (int)gb ? *reinterpret_cast<const uint4 *>(qbase + (size_t)h * hd + 8 * pc)
+                                        : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
                 for (int h = 0; h < ATT_GMAX; ++h) {
                     if (h >= (int)gb) break;
-                    const float4 qa = *reinterpret_cast<const float4 *>(qs + h * hd + 8 * pc);
-                    const float4 qb = *reinterpret_cast<const float4 *>(qs + h * hd + 8 * pc + 4);
 #pragma unroll
                     for (int it = 0; it < 4; ++it) {
-                        const uint4 w = kv[it];
                         float a = acc[it][h];
-                        a += qa.x * __uint_as_float(w.x << 16) + qa.y * __uint_as_float(w.x & 0xffff0000u);
-                        a += qa.z * __uint_as_float(w.y << 16) + qa.w * __uint_as_float(w.y & 0xffff0000u);
-                        a += qb.x * __uint_as_float(w.z << 16) + qb.y * __uint_as_float(w.z & 0xffff0000u);
-                        a += qb.z * __uint_as_float(w.w << 16) + qb.w * __uint_as_float(w.w & 0xffff0000u);
+                        a = dot2_bf16(qv[h].x, kv[it].x, a);
+                        a = dot2_bf16(qv[h].y, kv[it].y, a);
+                        a = dot2_bf16(qv[h].z, kv[it].z, a);
+                        a = dot2_bf16(qv[h].w, kv[it].w, a);
                         acc[it][h] = a;
                     }
                 }
@@ -242,7 +252,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
         } else {
             const uint32_t npc = hd / 2;
             for (uint32_t pc = l16; pc < npc; pc += 16) {
-                uint32_t kv[4];
+                uint32_t kv[4], qv[ATT_GMAX];
 #pragma unroll
                 for (int it = 0; it < 4; ++it) {
                     const uint32_t jj = wave * 16 + it * 4 + rg;
@@ -250,12 +260,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
                                     : 0u;
                 }
 #pragma unroll
+                for (int h = 0; h < ATT_GMAX; ++h)
+                    qv[h] = h < (int)gb ? *reinterpret_cast<const uint32_t *>(qbase + (size_t)h * hd + 2 * pc) : 0u;
+#pragma unroll
                 for (int h = 0; h < ATT_GMAX; ++h) {
                     if (h >= (int)gb) break;
-                    const float2 qa = *reinterpret_cast<const float2 *>(qs + h * hd + 2 * pc);
 #pragma unroll
-                    for (int it = 0; it < 4; ++it)
-                        acc[it][h] += qa.x * __uint_as_float(kv[it] << 16) + qa.y * __uint_as_float(kv[it] & 0xffff0000u);
+                    for (int it = 0; it < 4; ++it) acc[it][h] = dot2_bf16(qv[h], kv[it], acc[it][h]);
                 }
             }
         }
@@ -270,13 +281,25 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
             }
         }
         __syncthreads();
-        // Running max and sum: wave w owns heads w and w + 4.
-        for (uint32_t h = wave; h < gb; h += 4) {
-            const float v = sc[h][lane];
-            const float mo = mrun[h], mn = fmaxf(mo, wave_max_f32(v));
-            const float p = lane < n ? expf(v - mn) : 0.0f;
-            const float ps = wave_sum_dpp(p);
-            sc[h][lane] = p;
+        // Running max and sum: wave h owns head h.
+        if (wave < gb) {
+            const uint32_t h = wave;
+            float v[ATT_TILE / 64];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < ATT_TILE / 64; ++i) {
+                v[i] = sc[h][lane + 64 * i];
+                mx = fmaxf(mx, v[i]);
+            }
+            const float mo = mrun[h], mn = fmaxf(mo, wave_max_f32(mx));
+            float ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < ATT_TILE / 64; ++i) {
+                const float p = lane + 64 * i < n ? expf(v[i] - mn) : 0.0f;
+                sc[h][lane + 64 * i] = p;
+                ps += p;
+            }
+            ps = wave_sum_dpp(ps);
             if (lane == 0) {
                 const float c = expf(mo - mn);   // 0 on the first tile (mo = -inf)
                 corr[h] = c;
@@ -291,26 +314,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
             for (int h = 0; h < ATT_GMAX; ++h) {
                 if (h >= (int)gb) break;
                 const float c = corr[h];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    o[h][e][0] *= c;
-                    o[h][e][1] *= c;
-                }
+                o[h][0] *= c;
+                o[h][1] *= c;
             }
-            const bool two = dp + ATT_THREADS < npairs;
-            auto accumulate = [&](uint32_t jj, uint32_t w0) {
-                const uint16_t *vr = vbase + (size_t)(t0 + jj) * pitch;
-                const uint32_t w1 = two ? *reinterpret_cast<const uint32_t *>(vr + 2 * (dp + ATT_THREADS)) : 0u;
-                const float a0 = __uint_as_float(w0 << 16), a1 = __uint_as_float(w0 & 0xffff0000u);
-                const float b0 = __uint_as_float(w1 << 16), b1 = __uint_as_float(w1 & 0xffff0000u);
+            auto accumulate = [&](uint32_t jj, uint32_t w) {
+                const float a0 = __uint_as_float(w << 16), a1 = __uint_as_float(w & 0xffff0000u);
 #pragma unroll
                 for (int h = 0; h < ATT_GMAX; ++h) {
                     if (h >= (int)gb) break;
                     const float p = sc[h][jj];
-                    o[h][0][0] += p * a0;
-                    o[h][0][1] += p * a1;
-                    o[h][1][0] += p * b0;
-                    o[h][1][1] += p * b1;
+                    o[h][0] += p * a0;
+                    o[h][1] += p * a1;
                 }
             };
 #pragma unroll
@@ -323,20 +337,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
         }
         __syncthreads();
     }
-    // Sum the row phases' o in LDS (the q copy is no longer read).
-    float *op = smem;   // [nph][gb][hd]
+    // Sum the row phases' o.
     if (active) {
 #pragma unroll
         for (int h = 0; h < ATT_GMAX; ++h) {
             if (h >= (int)gb) break;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const uint32_t d = 2 * (dp + e * ATT_THREADS);
-                if (d < hd) {
-                    op[((size_t)ph * gb + h) * hd + d] = o[h][e][0];
-                    op[((size_t)ph * gb + h) * hd + d + 1] = o[h][e][1];
-                }
-            }
+            op[((size_t)ph * gb + h) * hd + 2 * dp] = o[h][0];
+            op[((size_t)ph * gb + h) * hd + 2 * dp + 1] = o[h][1];
         }
     }
     __syncthreads();
@@ -357,13 +364,158 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split(
     }
 }
 
+// attention_split for head_dim % 8 == 0, head_dim <= 128 and 16-byte aligned
+// q, caches: a lane holds eight dimensions (one 16-byte piece) of a key row
+// and of the same value row, 16 lanes a row, so phase 2 accumulates the rows
+// phase 1 scored, from registers, eight dimensions per lane; the lanes of one
+// piece are summed across the wave (xor 16, 32) and across the waves in LDS.
+__global__ __launch_bounds__(ATT_THREADS) void attention_split16(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, uint32_t nh,
+    uint32_t nkv, uint32_t hd, uint32_t len, uint32_t chunk, uint32_t gb, float scale, float *__restrict__ part,
+    uint16_t *__restrict__ out) {
+    __shared__ float op[ATT_NW][ATT_GMAX][128];
+    __shared__ float sc[ATT_GMAX][ATT_TILE];
+    __shared__ float mrun[ATT_GMAX], lrun[ATT_GMAX], corr[ATT_GMAX];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t per_kv = nh / nkv, s = blockIdx.x;
+    const uint32_t h0 = gb == 1 ? (blockIdx.y % nkv) * per_kv + blockIdx.y / nkv : blockIdx.y * gb;
+    const uint32_t g = h0 / per_kv;
+    const size_t pitch = (size_t)nkv * hd;
+    const uint32_t j0 = s * chunk, j1 = min(len, j0 + chunk);
+    const uint32_t l16 = lane & 15, rg = lane >> 4, npc = hd / 8;
+    const bool piece = l16 < npc;   // lanes past the row's pieces load nothing
+    const uint16_t *kbase = kc + (size_t)g * hd + 8 * l16, *vbase = vc + (size_t)g * hd + 8 * l16;
+    uint4 qv[ATT_GMAX];
+#pragma unroll
+    for (int h = 0; h < ATT_GMAX; ++h)
+        qv[h] = piece && h < (int)gb ? *reinterpret_cast<const uint4 *>(q + (size_t)(h0 + h) * hd + 8 * l16)
+                                     : uint4{0u, 0u, 0u, 0u};
+    if (tid < ATT_GMAX) {
+        mrun[tid] = -INFINITY;
+        lrun[tid] = 0.0f;
+    }
+    float o[ATT_GMAX][8];
+#pragma unroll
+    for (int h = 0; h < ATT_GMAX; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+    __syncthreads();
+
+    for (uint32_t t0 = j0; t0 < j1; t0 += ATT_TILE) {
+        const uint32_t n = min((uint32_t)ATT_TILE, j1 - t0);
+        uint4 kv[4], vv[4];
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const uint32_t jj = wave * 16 + it * 4 + rg;
+            const bool ok = piece && jj < n;
+            const size_t off = (size_t)(t0 + jj) * pitch;
+            kv[it] = ok ? *reinterpret_cast<const uint4 *>(kbase + off) : uint4{0u, 0u, 0u, 0u};
+            vv[it] = ok ? *reinterpret_cast<const uint4 *>(vbase + off) : uint4{0u, 0u, 0u, 0u};
+        }
+        // Phase 1: scores of rows wave * 16 + it * 4 + rg.
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const uint32_t jj = wave * 16 + it * 4 + rg;
+#pragma unroll
+            for (int h = 0; h < ATT_GMAX; ++h) {
+                if (h >= (int)gb) break;
+                float a = dot2_bf16(qv[h].x, kv[it].x, 0.0f);
+                a = dot2_bf16(qv[h].y, kv[it].y, a);
+                a = dot2_bf16(qv[h].z, kv[it].z, a);
+                a = dot2_bf16(qv[h].w, kv[it].w, a);
+                a = row16_sum(a);
+                if (l16 == 15) sc[h][jj] = jj < n ? a * scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        if (wave < gb) {
+            const uint32_t h = wave;
+            float v[ATT_TILE / 64];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < ATT_TILE / 64; ++i) {
+                v[i] = sc[h][lane + 64 * i];
+                mx = fmaxf(mx, v[i]);
+            }
+            const float mo = mrun[h], mn = fmaxf(mo, wave_max_f32(mx));
+            float ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < ATT_TILE / 64; ++i) {
+                const float p = lane + 64 * i < n ? expf(v[i] - mn) : 0.0f;
+                sc[h][lane + 64 * i] = p;
+                ps += p;
+            }
+            ps = wave_sum_dpp(ps);
+            if (lane == 0) {
+                const float c = expf(mo - mn);   // 0 on the first tile (mo = -inf)
+                corr[h] = c;
+                lrun[h] = lrun[h] * c + ps;
+                mrun[h] = mn;
+            }
+        }
+        __syncthreads();
+        // Phase 2: the same rows' values, eight dimensions per lane.
+#pragma unroll
+        for (int h = 0; h < ATT_GMAX; ++h) {
+            if (h >= (int)gb) break;
+            const float c = corr[h];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[h][e] *= c;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const float p = sc[h][wave * 16 + it * 4 + rg];   // 0 past n
+                const uint4 w = vv[it];
+                o[h][0] += p * __uint_as_float(w.x << 16);
+                o[h][1] += p * __uint_as_float(w.x & 0xffff0000u);
+                o[h][2] += p * __uint_as_float(w.y << 16);
+                o[h][3] += p * __uint_as_float(w.y & 0xffff0000u);
+                o[h][4] += p * __uint_as_float(w.z << 16);
+                o[h][5] += p * __uint_as_float(w.z & 0xffff0000u);
+                o[h][6] += p * __uint_as_float(w.w << 16);
+                o[h][7] += p * __uint_as_float(w.w & 0xffff0000u);
+            }
+        }
+        __syncthreads();
+    }
+    // The four row groups of a wave, then the waves.
+#pragma unroll
+    for (int h = 0; h < ATT_GMAX; ++h) {
+        if (h >= (int)gb) break;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = o[h][e];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (rg == 0 && piece) op[wave][h][8 * l16 + e] = v;
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < gb * hd; i += ATT_THREADS) {
+        const uint32_t h = i / hd, d = i % hd;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < ATT_NW; ++w) v += op[w][h][d];
+        if (part == nullptr) {
+            out[(size_t)h0 * hd + i] = f32_bf16(v / lrun[h]);
+        } else {
+            part[((size_t)s * nh + h0) * hd + i] = v;
+        }
+    }
+    if (part != nullptr && tid < gb) {
+        float *ml = part + (size_t)gridDim.x * nh * hd;
+        ml[((size_t)s * nh + h0 + tid) * 2] = mrun[tid];
+        ml[((size_t)s * nh + h0 + tid) * 2 + 1] = lrun[tid];
+    }
+}
+
 // out_h = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s): the
-// splits of attention_split merged. One workgroup per head.
-__global__ __launch_bounds__(ATT_THREADS) void attention_combine(const float *__restrict__ part, uint32_t nh,
-                                                                 uint32_t hd, uint32_t splits,
-                                                                 uint16_t *__restrict__ out) {
+// splits of attention_split merged. One 256-thread workgroup per head.
+constexpr int COMBINE_THREADS = 256;
+__global__ __launch_bounds__(COMBINE_THREADS) void attention_combine(const float *__restrict__ part, uint32_t nh,
+                                                                     uint32_t hd, uint32_t splits,
+                                                                     uint16_t *__restrict__ out) {
     __shared__ float wsp[ATT_SPLIT_MAX];
-    __shared__ float red[4];
+    __shared__ float red[COMBINE_THREADS / 64];
     const uint32_t h = blockIdx.x, tid = threadIdx.x;
     const float *ml = part + (size_t)splits * nh * hd;
     const float m = tid < splits ? ml[((size_t)tid * nh + h) * 2] : -INFINITY;
@@ -372,7 +524,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_combine(const float *__
     const float den = block_sum(tid < splits ? w * ml[((size_t)tid * nh + h) * 2 + 1] : 0.0f, red);
     if (tid < splits) wsp[tid] = w / den;
     __syncthreads();
-    for (uint32_t d = tid; d < hd; d += ATT_THREADS) {
+    for (uint32_t d = tid; d < hd; d += COMBINE_THREADS) {
         float v = 0.0f;
 #pragma unroll 16
         for (uint32_t i = 0; i < splits; ++i) v += wsp[i] * part[((size_t)i * nh + h) * hd + d];
@@ -472,10 +624,12 @@ RENG_HIP_API int reng_hip_rope_append(uint16_t *q, const uint16_t *k, const uint
 namespace {
 
 // The largest divisor of the query heads per key/value head that is at most
-// ATT_GMAX: the heads one workgroup serves from one read of the cache.
-uint32_t head_group(size_t per_kv) {
+// ATT_GMAX: the heads one workgroup serves from one read of the cache; smaller
+// while that leaves fewer workgroups than CUs.
+uint32_t head_group(size_t per_kv, size_t splits, size_t n_heads) {
+    const size_t cus = (size_t)device_props().cus;
     for (size_t g = per_kv < (size_t)ATT_GMAX ? per_kv : (size_t)ATT_GMAX; g > 1; --g)
-        if (per_kv % g == 0) return (uint32_t)g;
+        if (per_kv % g == 0 && splits * (n_heads / g) >= cus) return (uint32_t)g;
     return 1;
 }
 
@@ -493,21 +647,26 @@ int attention_args(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v
                  RENG_HIP_ATTENTION_MAX_LEN);
     RENG_REQUIRE(n_heads <= 0x7fffffff, "too many heads");
     RENG_REQUIRE(q && k_cache && v_cache && out, "null pointer");
-    RENG_REQUIRE((reinterpret_cast<uintptr_t>(k_cache) & 3) == 0 && (reinterpret_cast<uintptr_t>(v_cache) & 3) == 0,
-                 "k_cache and v_cache must be 4-byte aligned");
+    RENG_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
+                   reinterpret_cast<uintptr_t>(v_cache)) & 3) == 0,
+                 "q, k_cache and v_cache must be 4-byte aligned");
     return RENG_HIP_OK;
 }
 
 int launch_attention(const uint16_t *q, const uint16_t *kc, const uint16_t *vc, size_t nh, size_t nkv, size_t hd,
                      size_t len, float scale, float *part, uint16_t *out, hipStream_t st) {
     const AttnPlan p = attn_plan(len, part != nullptr);
-    const uint32_t gb = p.splits > 1 ? head_group(nh / nkv) : 1u;
+    const uint32_t gb = p.splits > 1 ? head_group(nh / nkv, p.splits, nh) : 1u;
     const size_t npairs = hd / 2, dpb = npairs < (size_t)ATT_THREADS ? npairs : (size_t)ATT_THREADS;
     const size_t lds = (ATT_THREADS / dpb) * gb * hd * sizeof(float);
-    const bool v8 = hd % 8 == 0 && (reinterpret_cast<uintptr_t>(kc) & 15) == 0;
+    const bool v8 = hd % 8 == 0 && ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(q)) & 15) == 0;
+    const bool v16 = v8 && hd <= 128 && (reinterpret_cast<uintptr_t>(vc) & 15) == 0;
     float *wp = p.splits > 1 ? part : nullptr;
     const dim3 grid(p.splits, (unsigned)(nh / gb));
-    if (v8)
+    if (v16)
+        hipLaunchKernelGGL(attention_split16, grid, dim3(ATT_THREADS), 0, st, q, kc, vc, (uint32_t)nh, (uint32_t)nkv,
+                           (uint32_t)hd, (uint32_t)len, p.chunk, gb, scale, wp, out);
+    else if (v8)
         hipLaunchKernelGGL(attention_split<true>, grid, dim3(ATT_THREADS), lds, st, q, kc, vc, (uint32_t)nh,
                            (uint32_t)nkv, (uint32_t)hd, (uint32_t)len, p.chunk, gb, scale, wp, out);
     else
@@ -515,7 +674,7 @@ int launch_attention(const uint16_t *q, const uint16_t *kc, const uint16_t *vc, 
                            (uint32_t)nkv, (uint32_t)hd, (uint32_t)len, p.chunk, gb, scale, wp, out);
     if (int rc = check_launch("attention_split")) return rc;
     if (p.splits < 2) return RENG_HIP_OK;
-    hipLaunchKernelGGL(attention_combine, dim3((unsigned)nh), dim3(ATT_THREADS), 0, st, wp, (uint32_t)nh,
+    hipLaunchKernelGGL(attention_combine, dim3((unsigned)nh), dim3(COMBINE_THREADS), 0, st, wp, (uint32_t)nh,
                        (uint32_t)hd, p.splits, out);
     return check_launch("attention_combine");
 }
@@ -533,9 +692,9 @@ RENG_HIP_API int reng_hip_attention_decode(const uint16_t *q, const uint16_t *k_
 
 RENG_HIP_API size_t reng_hip_attention_workspace_bytes(size_t n_heads, size_t head_dim, size_t len) {
     if (len > RENG_HIP_ATTENTION_MAX_LEN) len = RENG_HIP_ATTENTION_MAX_LEN;
+    if (len <= (size_t)ATT_ONE_PASS_MAX || n_heads > 0x7fffffff || head_dim > 1024) return 0;
     size_t s = (len + ATT_SPLIT_ROWS - 1) / ATT_SPLIT_ROWS;
     if (s > (size_t)ATT_SPLIT_MAX) s = ATT_SPLIT_MAX;
-    if (n_heads > 0x7fffffff || head_dim > 1024) return 0;
     return split_part_bytes(s, n_heads, head_dim);
 }
 

@@ -217,9 +217,10 @@ def test_decode_step_entry_points_refuse_bad_arguments():
                                          None) == R.EINVAL                                # misaligned v_cache
     # The split form: its workspace covers every length up to the one asked for.
     need = lib.reng_hip_attention_workspace_bytes(4, 64, 700)
-    assert need == 22 * 4 * 66 * 4                      # ceil(700 / 32) = 22 splits of (o, m, l) per head
-    assert lib.reng_hip_attention_workspace_bytes(4, 64, 32) == 0
-    assert lib.reng_hip_attention_workspace_bytes(32, 128, 4096) == 64 * 32 * 130 * 4
+    assert need == 3 * 4 * 66 * 4                       # ceil(700 / 256) = 3 splits of (o, m, l) per head
+    assert lib.reng_hip_attention_workspace_bytes(4, 64, 512) == 0   # one pass
+    assert lib.reng_hip_attention_workspace_bytes(4, 64, 513) == 3 * 4 * 66 * 4
+    assert lib.reng_hip_attention_workspace_bytes(32, 128, 4096) == 16 * 32 * 130 * 4
     assert lib.reng_hip_attention_workspace_bytes(32, 128, 10 ** 9) == 64 * 32 * 130 * 4
     assert lib.reng_hip_attention_decode_split(p, p, p, 4, 2, 64, 700, 1.0, p, need - 4, p, None) == R.EINVAL
     assert b"workspace of" in lib.reng_hip_last_error()
@@ -408,12 +409,12 @@ def _attention_want(Q, K, V, nh, nkv, hd, scale):
 @pytest.mark.parametrize("nh,nkv,hd", [(6, 2, 64), (32, 8, 128), (4, 4, 6), (2, 1, 1024), (16, 1, 128)])
 def test_attention_forms_against_numpy(nh, nkv, hd):
     """Both attention entry points against float64 numpy softmax attention:
-    lengths around the split threshold (32 rows) and the 64-row tile, long
-    caches that take 64 splits, head_dim not a multiple of 8 (the 4-byte
-    key path), head_dim 1024 (two value pairs per thread), one key/value head
-    for 16 query heads (head groups of 8), and a key cache 4 bytes off a
-    16-byte boundary (the 4-byte key path at head_dim % 8 == 0). The split
-    form's workspace starts as NaN, so a split it fails to write shows up."""
+    lengths around the 256-row tile and the one-pass limit (512 rows), caches
+    that take several tiles per split and 64 splits, head_dim not a multiple
+    of 8 (the 4-byte key path), head_dim 1024, one key/value head for 16 query
+    heads, and a key cache 4 bytes off a 16-byte boundary (the 4-byte key path
+    at head_dim % 8 == 0). The split form's workspace starts as NaN, so a split
+    it fails to write shows up."""
     import torch
 
     import reng_hip as R
@@ -422,7 +423,7 @@ def test_attention_forms_against_numpy(nh, nkv, hd):
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
     scale = hd ** -0.5
-    lengths = (1, 31, 32, 33, 64, 65, 700, 5000) if hd <= 128 else (1, 33, 700)
+    lengths = (1, 33, 255, 256, 257, 512, 513, 700, 5000, 20000) if hd <= 128 else (1, 33, 700)
     ws = torch.full((R.attention_workspace_bytes(nh, hd, max(lengths)) // 4 + 1,), float("nan"),
                     dtype=torch.float32, device="cuda")
     for length in lengths:
@@ -439,7 +440,7 @@ def test_attention_forms_against_numpy(nh, nkv, hd):
         assert O.rel_l2(one, want) < 4e-3, (length, "one pass")
         assert O.rel_l2(split, want) < 4e-3, (length, "split")
         # the same key cache 4 bytes past a 16-byte boundary
-        if hd % 8 == 0 and length in (33, 700):
+        if hd % 8 == 0 and length in (33, 700, 5000):
             kk = torch.zeros(dk.numel() + 2, dtype=torch.int16, device="cuda")
             kk[2:] = dk
             off = bf16_f32(bits(R.attention_decode_split(dq, kk[2:], dv, nh, nkv, hd, length, scale, workspace=ws)))
