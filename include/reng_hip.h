@@ -219,6 +219,24 @@ RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm_swiglu(const float *x, const float 
                                                     const uint8_t *codes, const float *scales, size_t N, size_t K,
                                                     int format, uint16_t *y, void *stream);
 
+/* A decode step's first projection in one pass: n = bf16(rms_norm(x) * gamma),
+ * [q | k | v] = bf16(n W^T), q and k rotated (rotate-half RoPE with this
+ * position's sin_row / cos_row [head_dim] rows of the tables) into q
+ * [n_heads * head_dim] and k_row [n_kv_heads * head_dim], v copied into v_row
+ * (k_row and v_row: this position's rows of the key and value caches).
+ * codes / scales hold the N = (n_heads + 2 n_kv_heads) head_dim rows of
+ * [Wq; Wk; Wv] in rotation-pair order: with half = head_dim / 2, row
+ * 2 (h half + d) and row 2 (h half + d) + 1 are Wq rows h head_dim + d and
+ * h head_dim + d + half (h < n_heads, d < half); the k heads follow the same
+ * way from row 2 n_heads half; then the Wv rows in their order. Bit-identical
+ * to reng_hip_gemv_w8a16_rmsnorm over [Wq; Wk; Wv] then reng_hip_rope_append.
+ * x and gamma f32 [K], K % 16 == 0, K <= 32768; head_dim even. */
+RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm_qkv_rope(const float *x, const float *gamma, float eps,
+                                                      const uint8_t *codes, const float *scales, size_t n_heads,
+                                                      size_t n_kv_heads, size_t head_dim, size_t K, int format,
+                                                      const float *sin_row, const float *cos_row, uint16_t *q,
+                                                      uint16_t *k_row, uint16_t *v_row, void *stream);
+
 /* h = x + d and out = bf16(rms_norm(h) * gamma) in one pass, x and h f32, d
  * bf16 [rows, cols] (a branch output added to the residual stream, then the
  * next sublayer's RMSNorm; h must not overlap x or d). */

@@ -363,6 +363,30 @@ RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm_swiglu(const float *x, const float 
     return gemv_norm(x, gamma, eps, codes, scales, N, K, format, true, y, stream);
 }
 
+RENG_HIP_API int reng_hip_gemv_w8a16_rmsnorm_qkv_rope(const float *x, const float *gamma, float eps,
+                                                      const uint8_t *codes, const float *scales, size_t n_heads,
+                                                      size_t n_kv_heads, size_t head_dim, size_t K, int format,
+                                                      const float *sin_row, const float *cos_row, uint16_t *q,
+                                                      uint16_t *k_row, uint16_t *v_row, void *stream) {
+    clear_error();
+    RENG_REQUIRE(valid_format(format), "unknown fp8 format %d", format);
+    RENG_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                 "%zu query heads are not a multiple of %zu key/value heads", n_heads, n_kv_heads);
+    RENG_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 1024, "head_dim %zu is not even in [2, 1024]",
+                 head_dim);
+    RENG_REQUIRE(K > 0 && K % 16 == 0, "K = %zu is not a positive multiple of 16", K);
+    RENG_REQUIRE(K <= 32768, "K = %zu is past 32768 (the normalised row is staged in 64 KB of LDS)", K);
+    RENG_REQUIRE((n_heads + 2 * n_kv_heads) * head_dim <= 0x7fffffff, "dimension too large");
+    RENG_REQUIRE(eps >= 0.0f, "eps %g is negative", (double)eps);
+    RENG_REQUIRE(x && gamma && codes && sin_row && cos_row && q && k_row && v_row, "null pointer");
+    RENG_REQUIRE((reinterpret_cast<uintptr_t>(codes) & 15) == 0, "codes must be 16-byte aligned");
+    RENG_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma)) & 3) == 0,
+                 "x and gamma must be 4-byte aligned");
+    return launch_gemv_norm_rope(x, gamma, eps, codes, scales, (uint32_t)n_heads, (uint32_t)n_kv_heads,
+                                 (uint32_t)head_dim, (uint32_t)K, format, sin_row, cos_row, q, k_row, v_row,
+                                 as_stream(stream));
+}
+
 RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const float *scale_a,
                                           size_t n_scale_a, const uint8_t *b, int b_format,
                                           const float *scale_b, size_t n_scale_b, size_t M,

@@ -231,6 +231,18 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
+// ---------------------------------------------------------------- RoPE
+
+// Rotate-half RoPE of one dimension pair (d, d + half) (rope_cpu,
+// crates/reng-synapse/src/ops.rs:118-135): o0 = x0 cos[d] - x1 sin[d],
+// o1 = x1 cos[d + half] + x0 sin[d + half], with the fused multiply-adds
+// spelled out so that every kernel that rotates rounds the same way.
+__device__ __forceinline__ void rope_rotate(float x0, float x1, float c0, float s0, float c1, float s1, float &o0,
+                                            float &o1) {
+    o0 = fmaf(x0, c0, -(x1 * s0));
+    o1 = fmaf(x1, c1, x0 * s1);
+}
+
 // ---------------------------------------------------------------- RMSNorm
 
 // 1 / sqrt(mean(h^2) + eps) of a row h[0, cols) (rms_norm_cpu,

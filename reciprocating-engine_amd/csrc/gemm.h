@@ -19,6 +19,11 @@ int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *sca
 // plain or the SwiGLU-pair epilogue.
 int launch_gemv_norm(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
                      uint32_t N, uint32_t K, int format, bool swiglu, uint16_t *y, hipStream_t st);
+// The RMSNorm prologue over a [q; k; v] projection whose rows come in rotation pairs, with RoPE and the
+// cache-row writes as the epilogue (N = (nh + 2 nkv) hd).
+int launch_gemv_norm_rope(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
+                          uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t K, int format, const float *sin_row,
+                          const float *cos_row, uint16_t *q, uint16_t *k_row, uint16_t *v_row, hipStream_t st);
 // 4 < M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st);

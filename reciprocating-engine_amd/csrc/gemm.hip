@@ -2,8 +2,8 @@
 //
 // 1. gemv_w8a16     (M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
 //                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]); with
-//                    M = 1 also a residual-add epilogue, a SwiGLU-pair one and
-//                    an RMSNorm prologue.
+//                    M = 1 also residual-add, SwiGLU-pair and RoPE-pair
+//                    epilogues and an RMSNorm prologue.
 //    Streams the codes once with 16-byte loads, decodes in registers
 //    (v_cvt_pk_f32_fp8 / _bf8), f32 FMA, one wave per output row.
 // 2. The other M <= 64: the same product on bf16 MFMA with the codes and the
@@ -94,7 +94,36 @@ __device__ __forceinline__ void decode16(const u32x4 &q, uint32_t (&w)[8]) {
 // both rows of a pair, and y[i] = bf16(silu(bf16 gate) * bf16 up). Each is the
 // arithmetic of add_bf16_f32 / silu_mul_bf16 (layer.hip) after the plain
 // GEMV: a row's sum does not depend on which wave computes it.
-enum { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+//
+// EPI_ROPE takes the rows of a stacked [q; k; v] projection in rotation pairs
+// (row 2p, 2p + 1 = dimensions d, d + half of one q or k head, then v rows two
+// by two; RopeOut gives the order) and writes the pair rotated into q and the
+// key cache row, or copied into the value cache row: rope_append (layer.hip)
+// after the plain GEMV, through the same rope_rotate.
+enum { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ROPE = 3 };
+
+struct RopeOut {
+    uint16_t *q, *k_row, *v_row;   // [nh * hd], [nkv * hd], [nkv * hd] bf16
+    const float *sn, *cs;          // this position's rows of the tables, [hd]
+    uint32_t half, q_pairs, qk_pairs;   // hd / 2, nh * half, (nh + nkv) * half
+};
+
+__device__ __forceinline__ void rope_store(const RopeOut &ro, uint32_t p, uint32_t b0, uint32_t b1) {
+    if (p < ro.qk_pairs) {
+        const bool isq = p < ro.q_pairs;
+        const uint32_t pp = isq ? p : p - ro.q_pairs, head = pp / ro.half, d = pp % ro.half;
+        float o0, o1;
+        rope_rotate(__uint_as_float(b0 << 16), __uint_as_float(b1 << 16), ro.cs[d], ro.sn[d], ro.cs[d + ro.half],
+                    ro.sn[d + ro.half], o0, o1);
+        uint16_t *dst = (isq ? ro.q : ro.k_row) + (size_t)head * 2 * ro.half + d;
+        dst[0] = (uint16_t)f32_to_bf16_bits(o0);
+        dst[ro.half] = (uint16_t)f32_to_bf16_bits(o1);
+    } else {
+        const uint32_t i = p - ro.qk_pairs;
+        ro.v_row[2 * i] = (uint16_t)b0;
+        ro.v_row[2 * i + 1] = (uint16_t)b1;
+    }
+}
 
 __device__ __forceinline__ uint16_t silu_mul_bits(uint32_t g, uint32_t u) {
     const float gv = __uint_as_float(g << 16), uv = __uint_as_float(u << 16);
@@ -114,10 +143,11 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
                                                   const uint8_t *__restrict__ codes,
                                                   const float *__restrict__ scales, uint32_t N,
                                                   uint32_t K, uint16_t *__restrict__ y, const float *res,
-                                                  float *yres, const float *__restrict__ gamma, float eps) {
+                                                  float *yres, const float *__restrict__ gamma, float eps,
+                                                  RopeOut ro) {
     static_assert(EPI == EPI_PLAIN || M == 1, "the fused epilogues take one activation row");
     static_assert(PRO == PRO_NONE || (M == 1 && XLDS), "the RMSNorm prologue stages one row in LDS");
-    constexpr bool PAIRS = EPI == EPI_SWIGLU;
+    constexpr bool PAIRS = EPI == EPI_SWIGLU || EPI == EPI_ROPE;
     extern __shared__ __attribute__((aligned(16))) uint32_t xs[];
     __shared__ float red[PRO == PRO_NONE ? 1 : NORM_VT / 64];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -185,7 +215,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
         __syncthreads();
     }
     if (r >= N) return;
-    uint32_t gate_bits = 0;   // EPI_SWIGLU: the pair's gate, held until its up row ends
+    uint32_t gate_bits = 0;   // PAIRS: the pair's first row, held until its second row ends
     float acc[M][2];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
@@ -246,6 +276,13 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
                     const uint32_t b = f32_to_bf16_bits(t * s);
                     if (r & 1) {
                         if (lane == 0) y[r >> 1] = silu_mul_bits(gate_bits, b);
+                    } else {
+                        gate_bits = b;
+                    }
+                } else if constexpr (EPI == EPI_ROPE) {
+                    const uint32_t b = f32_to_bf16_bits(t * s);
+                    if (r & 1) {
+                        if (lane == 0) rope_store(ro, r >> 1, gate_bits, b);
                     } else {
                         gate_bits = b;
                     }
@@ -331,15 +368,16 @@ GemvPlan gemv_plan(uint32_t M, uint32_t N, uint32_t K, uint32_t unit) {
 
 template <int F, int EPI, int PRO = PRO_NONE>
 int launch_gemv_epi_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
-                      uint16_t *y, const float *res, float *yres, const float *gamma, float eps, hipStream_t st) {
-    const GemvPlan p = gemv_plan(1, N, K, EPI == EPI_SWIGLU ? 2 : 1);
+                      uint16_t *y, const float *res, float *yres, const float *gamma, float eps, hipStream_t st,
+                      const RopeOut &ro = RopeOut{}) {
+    const GemvPlan p = gemv_plan(1, N, K, EPI == EPI_SWIGLU || EPI == EPI_ROPE ? 2 : 1);
     if (PRO != PRO_NONE && !p.xlds) {
         set_error("K = %u: the RMSNorm prologue stages the row in 64 KB of LDS (K <= 32768)", K);
         return RENG_HIP_EINVAL;
     }
 #define RENG_GEMV_E(C, XL, RG)                                                                                  \
     hipLaunchKernelGGL((gemv_w8a16<F, 1, C, XL, RG, EPI, PRO>), dim3(p.blocks), dim3(GemvPlan::threads), p.lds, \
-                       st, x, codes, scales, N, K, y, res, yres, gamma, eps)
+                       st, x, codes, scales, N, K, y, res, yres, gamma, eps, ro)
     if constexpr (PRO != PRO_NONE) {
         if (p.cpl7) RENG_GEMV_E(7, true, false);
         else if (p.ragged) RENG_GEMV_E(4, true, true);
@@ -354,6 +392,7 @@ int launch_gemv_epi_t(const uint16_t *x, const uint8_t *codes, const float *scal
     }
 #undef RENG_GEMV_E
     return check_launch(EPI == EPI_SWIGLU ? "gemv_w8a16 (SwiGLU pairs)"
+                        : EPI == EPI_ROPE  ? "gemv_w8a16 (RoPE pairs)"
                         : EPI == EPI_RESID ? "gemv_w8a16 (residual)"
                                            : "gemv_w8a16 (RMSNorm)");
 }
@@ -366,6 +405,35 @@ int launch_gemv_norm_t(const float *x, const float *gamma, float eps, const uint
         K % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma)) & 15) == 0;
     return vec ? launch_gemv_epi_t<F, EPI, PRO_NORM_VEC>(xa, codes, scales, N, K, y, nullptr, nullptr, gamma, eps, st)
                : launch_gemv_epi_t<F, EPI, PRO_NORM>(xa, codes, scales, N, K, y, nullptr, nullptr, gamma, eps, st);
+}
+
+template <int F>
+int launch_gemv_norm_rope_t(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
+                            uint32_t N, uint32_t K, const RopeOut &ro, hipStream_t st) {
+    const uint16_t *xa = reinterpret_cast<const uint16_t *>(x);
+    const bool vec =
+        K % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma)) & 15) == 0;
+    return vec ? launch_gemv_epi_t<F, EPI_ROPE, PRO_NORM_VEC>(xa, codes, scales, N, K, nullptr, nullptr, nullptr,
+                                                               gamma, eps, st, ro)
+               : launch_gemv_epi_t<F, EPI_ROPE, PRO_NORM>(xa, codes, scales, N, K, nullptr, nullptr, nullptr, gamma,
+                                                           eps, st, ro);
+}
+
+int launch_gemv_norm_rope(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
+                          uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t K, int format, const float *sin_row,
+                          const float *cos_row, uint16_t *q, uint16_t *k_row, uint16_t *v_row, hipStream_t st) {
+    RopeOut ro;
+    ro.q = q;
+    ro.k_row = k_row;
+    ro.v_row = v_row;
+    ro.sn = sin_row;
+    ro.cs = cos_row;
+    ro.half = hd / 2;
+    ro.q_pairs = nh * ro.half;
+    ro.qk_pairs = (nh + nkv) * ro.half;
+    const uint32_t N = (nh + 2 * nkv) * hd;
+    return format == RENG_HIP_E4M3 ? launch_gemv_norm_rope_t<RENG_HIP_E4M3>(x, gamma, eps, codes, scales, N, K, ro, st)
+                                   : launch_gemv_norm_rope_t<RENG_HIP_E5M2>(x, gamma, eps, codes, scales, N, K, ro, st);
 }
 
 int launch_gemv_norm(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
@@ -421,7 +489,7 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
         const bool xlds = p.xlds, cpl7 = p.cpl7, ragged = p.ragged;
 #define RENG_GEMV(MM, C, XL, RG)                                                                   \
     hipLaunchKernelGGL((gemv_w8a16<F, MM, C, XL, RG>), dim3(blocks), dim3(threads), lds, st, x, codes, \
-                       scales, N, K, y, nullptr, nullptr, nullptr, 0.0f)
+                       scales, N, K, y, nullptr, nullptr, nullptr, 0.0f, RopeOut{})
 #define RENG_GEMV_X(MM, C, RG) \
     if (xlds) RENG_GEMV(MM, C, true, RG); else RENG_GEMV(MM, C, false, RG);
 #define RENG_GEMV_M(MM)                                  \

@@ -107,8 +107,8 @@ __global__ __launch_bounds__(64) void rope_append(uint16_t *__restrict__ q, cons
     }
     for (uint32_t d = threadIdx.x; d < half; d += blockDim.x) {
         const float x0 = bf16_f32(src[d]), x1 = bf16_f32(src[d + half]);
-        const float o0 = x0 * cs[d] - x1 * sn[d];
-        const float o1 = x1 * cs[d + half] + x0 * sn[d + half];
+        float o0, o1;
+        rope_rotate(x0, x1, cs[d], sn[d], cs[d + half], sn[d + half], o0, o1);
         dst[d] = f32_bf16(o0);
         dst[d + half] = f32_bf16(o1);
     }

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
+#include <cstring>
 #include <initializer_list>
 #include <string>
 
@@ -112,6 +113,40 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
             }
             return m;
         };
+        // q, k and v rows stacked in rotation-pair order
+        // (reng_hip_gemv_w8a16_rmsnorm_qkv_rope): the (d, d + half) rows of
+        // each q head, then of each k head, then the v rows.
+        auto qkv_rope = [&](const LayerFp8 &f) {
+            if (abi_format(f.wk.format) != abi_format(f.wq.format) ||
+                abi_format(f.wv.format) != abi_format(f.wq.format))
+                throw Error("Fp8Decoder: projections of one input row carry different fp8 formats");
+            Mat m;
+            m.rows = qd + 2 * kvd;
+            m.cols = hidden_;
+            m.format = abi_format(f.wq.format);
+            std::vector<uint8_t> codes(m.rows * m.cols);
+            std::vector<float> scales(m.rows);
+            size_t r = 0;
+            auto put = [&](const reng_fp8::Quantized &q, size_t src) {
+                std::memcpy(&codes[r * m.cols], &q.codes[src * m.cols], m.cols);
+                scales[r++] = q.scales[src];
+            };
+            const size_t half = hd_ / 2;
+            for (size_t h = 0; h < nh_; ++h)
+                for (size_t d = 0; d < half; ++d) {
+                    put(f.wq, h * hd_ + d);
+                    put(f.wq, h * hd_ + d + half);
+                }
+            for (size_t g = 0; g < nkv_; ++g)
+                for (size_t d = 0; d < half; ++d) {
+                    put(f.wk, g * hd_ + d);
+                    put(f.wk, g * hd_ + d + half);
+                }
+            for (size_t i = 0; i < kvd; ++i) put(f.wv, i);
+            m.codes = static_cast<uint8_t *>(upload(codes.data(), codes.size()));
+            m.scales = static_cast<float *>(upload(scales.data(), scales.size() * sizeof(float)));
+            return m;
+        };
         for (size_t li = 0; li < w.layers.size(); ++li) {
             const LayerFp8 &f = (*w.fp8)[li];
             const LayerTensors &t = w.layers[li];
@@ -123,7 +158,7 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
             check(f.wu, inter_, hidden_, "wu");
             check(f.wd, hidden_, inter_, "wd");
             Layer L;
-            L.wqkv = mat({&f.wq, &f.wk, &f.wv});
+            L.wqkv = qkv_rope(f);
             L.wo = mat({&f.wo});
             L.wgu = mat({&f.wg, &f.wu}, true);
             L.wd = mat({&f.wd});
@@ -150,9 +185,7 @@ Fp8Decoder::Fp8Decoder(const LlamaConfig &cfg, const LlamaWeights &w, size_t max
         x_ = static_cast<float *>(dev(hidden_ * 4));
         h_ = static_cast<float *>(dev(hidden_ * 4));
         // bf16 buffers 16-byte aligned (hipMalloc) for the GEMV's inputs.
-        q_ = static_cast<uint16_t *>(dev((qd + 2 * kvd) * 2));   // q | k | v, one GEMV's output
-        k_ = q_ + qd;
-        v_ = k_ + kvd;
+        q_ = static_cast<uint16_t *>(dev(qd * 2));
         a_ = static_cast<uint16_t *>(dev(qd * 2));
         act_ = static_cast<uint16_t *>(dev(inter_ * 2));
         attn_ws_bytes_ = reng_hip_attention_workspace_bytes(nh_, hd_, max_pos_);
@@ -176,12 +209,11 @@ void Fp8Decoder::step_device(size_t li, const float *x, float *y, size_t pos, vo
                     ", asked for " + std::to_string(pos));
     if (pos >= max_pos_) throw Error("Fp8Decoder: position " + std::to_string(pos) + " is past the cache");
     const size_t kvd = nkv_ * hd_;
-    // Norm + q/k/v; RoPE and the cache append; attention; o-proj + residual
+    // Norm + q/k/v + RoPE + the cache append; attention; o-proj + residual
     // (h); norm + gate/up + SiLU * up; down + residual (y).
-    abi_ok(reng_hip_gemv_w8a16_rmsnorm(x, L.g1, eps_, L.wqkv.codes, L.wqkv.scales, L.wqkv.rows, L.wqkv.cols,
-                                       L.wqkv.format, q_, stream));
-    abi_ok(reng_hip_rope_append(q_, k_, v_, nh_, nkv_, hd_, sin_ + pos * hd_, cos_ + pos * hd_,
-                                L.kcache + pos * kvd, L.vcache + pos * kvd, stream));
+    abi_ok(reng_hip_gemv_w8a16_rmsnorm_qkv_rope(x, L.g1, eps_, L.wqkv.codes, L.wqkv.scales, nh_, nkv_, hd_, hidden_,
+                                                L.wqkv.format, sin_ + pos * hd_, cos_ + pos * hd_, q_,
+                                                L.kcache + pos * kvd, L.vcache + pos * kvd, stream));
     abi_ok(reng_hip_attention_decode_split(q_, L.kcache, L.vcache, nh_, nkv_, hd_, pos + 1, scale_, attn_ws_,
                                            attn_ws_bytes_, a_, stream));
     abi_ok(reng_hip_gemv_w8a16_residual(a_, L.wo.codes, L.wo.scales, L.wo.rows, L.wo.cols, L.wo.format, x, h_,

@@ -1,9 +1,9 @@
 // fp8_decoder.hpp - the device consumer of LlamaWeights::fp8: one decode step
 // (one token) of a Llama decoder layer whose seven projections are the fp8
-// GEMV over the layer's codes and per-row scales (q, k and v as one GEMV over
-// their stacked rows; gate and up as one over their rows alternating, with
-// silu(gate) * up as its epilogue; down with the residual add as its
-// epilogue).
+// GEMV over the layer's codes and per-row scales (q, k and v as one GEMV with
+// the RMSNorm as its prologue and RoPE and the cache append as its epilogue;
+// gate and up as one over their rows alternating, with silu(gate) * up as its
+// epilogue; o and down with the residual add as their epilogue).
 //
 // The reference quantizes on the host and then refuses at the point where the
 // codes would meet a device layer (layer_views, crates/reng-model/src/lib.rs:
@@ -62,7 +62,7 @@ class Fp8Decoder {
         int format = 0;
     };
     struct Layer {
-        Mat wqkv, wo, wgu, wd;   // q, k, v rows stacked; gate, up rows alternating
+        Mat wqkv, wo, wgu, wd;   // q, k, v rows in rotation pairs; gate, up rows alternating
         float *g1 = nullptr, *g2 = nullptr;
         uint16_t *kcache = nullptr, *vcache = nullptr;
         size_t pos = 0;
@@ -75,7 +75,7 @@ class Fp8Decoder {
     float *sin_ = nullptr, *cos_ = nullptr;
     // scratch: residual f32 rows, bf16 GEMV inputs and outputs
     float *x_ = nullptr, *h_ = nullptr;
-    uint16_t *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *a_ = nullptr;
+    uint16_t *q_ = nullptr, *a_ = nullptr;
     uint16_t *act_ = nullptr;
     // the split attention's partial outputs (one layer at a time)
     void *attn_ws_ = nullptr;

@@ -65,6 +65,8 @@ SIGNATURES = {
     "reng_hip_gemv_w8a16_swiglu": (_I, [_P, _P, _P, _SZ, _SZ, _I, _P, _P]),
     "reng_hip_gemv_w8a16_rmsnorm": (_I, [_P, _P, _F, _P, _P, _SZ, _SZ, _I, _P, _P]),
     "reng_hip_gemv_w8a16_rmsnorm_swiglu": (_I, [_P, _P, _F, _P, _P, _SZ, _SZ, _I, _P, _P]),
+    "reng_hip_gemv_w8a16_rmsnorm_qkv_rope": (_I, [_P, _P, _F, _P, _P, _SZ, _SZ, _SZ, _SZ, _I, _P, _P, _P, _P, _P,
+                                                   _P]),
     "reng_hip_rope_append": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P]),
     "reng_hip_attention_decode": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _P]),
     "reng_hip_attention_workspace_bytes": (_SZ, [_SZ, _SZ, _SZ]),
@@ -371,6 +373,32 @@ def gemv_rmsnorm(x, gamma, eps, codes, scales, n, k, fmt, swiglu=False, out=None
     _check(fn(_dev(x, "x"), _dev(gamma, "gamma"), eps, _dev(codes, "codes"),
               None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt), _dev(out, "out"), _stream()))
     return out
+
+
+def qkv_rope_row_order(n_heads, n_kv_heads, head_dim):
+    """Source row (in [Wq; Wk; Wv] order) of each row of the rotation-pair
+    order gemv_rmsnorm_qkv_rope takes."""
+    import numpy as np
+
+    half = head_dim // 2
+    order = []
+    for heads, base in ((n_heads, 0), (n_kv_heads, n_heads * head_dim)):
+        for h in range(heads):
+            for d in range(half):
+                order += [base + h * head_dim + d, base + h * head_dim + d + half]
+    order += list(range((n_heads + n_kv_heads) * head_dim, (n_heads + 2 * n_kv_heads) * head_dim))
+    return np.asarray(order, dtype=np.int64)
+
+
+def gemv_rmsnorm_qkv_rope(x, gamma, eps, codes, scales, n_heads, n_kv_heads, head_dim, k, fmt, sin_row, cos_row,
+                          q, k_row, v_row):
+    """Norm + [q | k | v] projection + RoPE + cache-row writes in one pass over
+    codes in qkv_rope_row_order."""
+    _check(lib().reng_hip_gemv_w8a16_rmsnorm_qkv_rope(
+        _dev(x, "x"), _dev(gamma, "gamma"), eps, _dev(codes, "codes"),
+        None if scales is None else _dev(scales, "scales"), n_heads, n_kv_heads, head_dim, k, _fmt(fmt),
+        _dev(sin_row, "sin_row"), _dev(cos_row, "cos_row"), _dev(q, "q"), _dev(k_row, "k_row"),
+        _dev(v_row, "v_row"), _stream()))
 
 
 def add_rms_norm_bf16(x, d, gamma, rows, cols, eps, h=None, out=None):

@@ -242,6 +242,11 @@ def test_decode_step_entry_points_refuse_bad_arguments():
     assert nm(ctypes.c_void_p(18), p, 1e-5, p, p, 8, 64, R.E4M3, p, None) == R.EINVAL   # x not 4-byte aligned
     assert nm(p, None, 1e-5, p, p, 8, 64, R.E4M3, p, None) == R.EINVAL                  # no gamma
     assert nms(p, p, 1e-5, p, p, 7, 64, R.E4M3, p, None) == R.EINVAL                    # odd N
+    qr = lib.reng_hip_gemv_w8a16_rmsnorm_qkv_rope
+    assert qr(p, p, 1e-5, p, p, 4, 2, 63, 64, R.E4M3, p, p, p, p, p, None) == R.EINVAL   # odd head_dim
+    assert qr(p, p, 1e-5, p, p, 6, 4, 64, 64, R.E4M3, p, p, p, p, p, None) == R.EINVAL   # 6 % 4
+    assert qr(p, p, 1e-5, p, p, 4, 2, 64, 32784, R.E4M3, p, p, p, p, p, None) == R.EINVAL
+    assert qr(p, p, 1e-5, p, p, 4, 2, 64, 64, R.E4M3, p, None, p, p, p, None) == R.EINVAL  # no cos_row
     assert lib.reng_hip_add_bf16_f32(p, None, 4, p, None) == R.EINVAL
 
 
@@ -393,6 +398,49 @@ def test_gemv_rmsnorm_prologue_equals_norm_then_gemv(fmt):
         want = bits(R.gemv_swiglu(normed, codes, scales, n, k, fmt))
         got = bits(R.gemv_rmsnorm(x, g, 1e-5, codes, scales, n, k, fmt, swiglu=True))
         assert np.array_equal(got, want), (n, k, shift, "swiglu")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_gemv_qkv_rope_equals_norm_gemv_then_rope(fmt):
+    """Norm + q/k/v + RoPE + cache-row writes in one pass against
+    gemv_rmsnorm over [Wq; Wk; Wv] then rope_append, bit for bit: Llama-3.1-8B
+    heads (32 / 8, head_dim 128, K = 4096), 6 / 2 heads of 64 over K = 1008,
+    and head_dim 6; only this position's cache rows are written."""
+    import torch
+
+    import layer as L
+    import reng_hip as R
+
+    rng = np.random.default_rng(9 if fmt == "e4m3" else 10)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    for nh, nkv, hd, k in ((32, 8, 128, 4096), (6, 2, 64, 1008), (4, 4, 6, 64)):
+        n = (nh + 2 * nkv) * hd
+        w = bf16_bits(rng.standard_normal((n, k)).astype(np.float32) * 0.05)
+        q = O.quantize_with(w, n, k, fmt, "pcs", 1.0)
+        codes = q.codes.reshape(n, k)
+        x = dev(rng.standard_normal(k).astype(np.float32) * 3)
+        g = dev((1 + rng.standard_normal(k) * 0.1).astype(np.float32))
+        pos, rows = 5, 8
+        sin, cos = L.rope_caches(rows, hd, 10000.0)
+        # the chain
+        qkv = R.gemv_rmsnorm(x, g, 1e-5, dev(codes.reshape(-1)), dev(q.scales), n, k, fmt)
+        qd, kvd = nh * hd, nkv * hd
+        kc = torch.zeros(rows * kvd, dtype=torch.int16, device="cuda")
+        vc = torch.zeros_like(kc)
+        R.rope_append(qkv[:qd], qkv[qd:qd + kvd], qkv[qd + kvd:], nh, nkv, hd, dev(sin[pos]), dev(cos[pos]),
+                      kc[pos * kvd:], vc[pos * kvd:])
+        # the fused pass over the rotation-pair order
+        order = R.qkv_rope_row_order(nh, nkv, hd)
+        fq = torch.empty(qd, dtype=torch.bfloat16, device="cuda")
+        fk = torch.zeros(rows * kvd, dtype=torch.int16, device="cuda")
+        fv = torch.zeros_like(fk)
+        R.gemv_rmsnorm_qkv_rope(x, g, 1e-5, dev(codes[order].reshape(-1)), dev(q.scales[order]), nh, nkv, hd, k,
+                                fmt, dev(sin[pos]), dev(cos[pos]), fq, fk[pos * kvd:], fv[pos * kvd:])
+        assert np.array_equal(bits(fq), bits(qkv[:qd])), (nh, nkv, hd)
+        assert np.array_equal(bits(fk), bits(kc)) and np.array_equal(bits(fv), bits(vc)), (nh, nkv, hd)
+        assert not bits(fk).reshape(rows, kvd)[pos + 1:].any() and not bits(fk).reshape(rows, kvd)[:pos].any()
 
 
 def _attention_want(Q, K, V, nh, nkv, hd, scale):
