@@ -122,6 +122,30 @@ def test_fp8_decode_step_matches_the_causal_cpu_layer(tmp_path, spec, fmt, schem
 
 
 @pytest.mark.gpu
+def test_fp8_decode_step_past_the_one_pass_attention_limit(tmp_path):
+    """600 positions: the attention takes one pass up to 512 cached rows and the
+    split + merge form after, with 16-byte key/value pieces at head_dim 32 and
+    two query heads per key/value head."""
+    hidden, inter, layers, heads, kv, tokens, theta = 128, 256, 1, 4, 2, 600, 10000.0
+    hd = hidden // heads
+    t = write_llama(str(tmp_path), hidden, inter, layers, heads, kv, 32, theta, seed=13)
+    x = np.random.default_rng(17).standard_normal((tokens, hidden)).astype(np.float32)
+    x.tofile(tmp_path / "in.f32")
+    r = subprocess.run([_built(), str(tmp_path), str(tmp_path / "in.f32"), str(tmp_path / "out.f32"), str(tokens),
+                        "--fp8", "e4m3:pcs"], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stdout + r.stderr
+    got = np.fromfile(tmp_path / "out.f32", dtype=np.float32).reshape(layers, tokens, hidden)
+    sin, cos = L.rope_caches(tokens, hd, theta)
+    w = oracle_layer_weights(t, 0, O.E4M3, "pcs")
+    want = L.layer(x, w, heads, kv, hd, 1e-5, sin, cos, hd ** -0.5)
+    branch = O.rel_l2((got[0] - x).ravel(), (want - x).ravel())
+    print(f"branch rel_L2 {branch:.2e}")
+    assert branch < 3e-2
+    for p in (0, 255, 256, 511, 512, 513, 599):
+        assert O.rel_l2((got[0, p] - x[p]), (want[p] - x[p])) < 6e-2, p
+
+
+@pytest.mark.gpu
 def test_decode_from_saved_codes_equals_the_fresh_quantize(tmp_path):
     """Codes written by reng-fp8-quantize --save and read back by
     load_weights_fp8_cached decode to the same bits as a fresh quantize."""
