@@ -284,6 +284,63 @@ def bench_decode_step(layers=4, positions=512):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+def cpu_decode_step(positions=512, steps=3):
+    """The CPU baseline beside the decode step: one token of a Llama-3.1-8B-shaped
+    layer at position positions - 1, in f32 over f32 weights, as the reference's
+    CPU decoder layer computes it (layer_cpu, crates/reng-synapse/src/model.rs:
+    2903-3100, in the oracle's restatement: its rms_norm, rope and silu; numpy
+    matrix-vector products on the host's BLAS threads), the key / value cache
+    holding positions - 1 earlier rows. Returns microseconds per layer-step (the
+    median of `steps`)."""
+    import numpy as np
+
+    import layer as L
+
+    h, inter, nh, nkv, hd, eps = 4096, 14336, 32, 8, 128, 1e-5
+    rng = np.random.default_rng(3)
+    mat = lambda rows, cols: rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+    w = {"wq": mat(nh * hd, h), "wk": mat(nkv * hd, h), "wv": mat(nkv * hd, h), "wo": mat(h, nh * hd),
+         "wg": mat(inter, h), "wu": mat(inter, h), "wd": mat(h, inter)}
+    g1 = np.ones(h, dtype=np.float32)
+    g2 = np.ones(h, dtype=np.float32)
+    p = positions - 1
+    kc = rng.standard_normal((positions, nkv * hd), dtype=np.float32)
+    vc = rng.standard_normal((positions, nkv * hd), dtype=np.float32)
+    sin, cos = L.rope_caches(positions, hd, 500000.0)
+    x = rng.standard_normal((1, h), dtype=np.float32)
+    scale = np.float32(hd ** -0.5)
+
+    def step():
+        n1 = L.rms_norm(x, g1, eps)
+        q = L.rope(n1 @ w["wq"].T, sin[p:p + 1], cos[p:p + 1], hd)
+        kc[p] = L.rope(n1 @ w["wk"].T, sin[p:p + 1], cos[p:p + 1], hd)[0]
+        vc[p] = (n1 @ w["wv"].T)[0]
+        a = np.empty((1, nh * hd), dtype=np.float32)
+        for hh in range(nh):
+            g = hh // (nh // nkv)
+            s_ = (kc[:, g * hd:(g + 1) * hd] @ q[0, hh * hd:(hh + 1) * hd]) * scale
+            e = np.exp(s_ - s_.max())
+            a[0, hh * hd:(hh + 1) * hd] = (e / e.sum()) @ vc[:, g * hd:(g + 1) * hd]
+        hres = x + a @ w["wo"].T
+        n2 = L.rms_norm(hres, g2, eps)
+        return hres + (L.silu(n2 @ w["wg"].T) * (n2 @ w["wu"].T)) @ w["wd"].T
+
+    step()
+    ts = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2] * 1e6
+
+
+def decode_cpu_record():
+    us = cpu_decode_step()
+    return {"us_per_layer_step": round(us, 1), "threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count())),
+            "kind": "port", "sample": "one token at position 511 of a Llama-3.1-8B-shaped layer, f32 weights, "
+            "the oracle's restatement of layer_cpu with numpy BLAS matrix-vector products (median of 3)"}
+
+
 def read_traffic(kind):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC
     summary (profiles/<kind>_traffic.txt: `fetch_bytes` and `write_bytes` lines,
@@ -349,6 +406,8 @@ def main():
                                                                            (27648, 5120), (5120, 27648))]
         elif args.part == "decode":
             out = [bench_decode_step()]
+            if not args.no_cpu:
+                out[0]["cpu_baseline"] = decode_cpu_record()
         else:
             out = [bench_f32_quantize(torch, R, gen)]
         log(json.dumps(out))
@@ -406,6 +465,8 @@ def main():
         log("prefill fp8:", extras["prefill_fp8_m1024_qwen32b"])
         torch.cuda.empty_cache()
         extras["decode_step_llama8b"] = bench_decode_step()
+        if not args.no_cpu and "error" not in extras["decode_step_llama8b"]:
+            extras["decode_step_llama8b"]["cpu_baseline"] = decode_cpu_record()
         log("decode step:", extras["decode_step_llama8b"])
         if args.extended:
             wq = WeightSet(torch, QWEN_32B, 64, seed=4321)
