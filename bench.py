@@ -441,7 +441,7 @@ def main():
     extras = {}
     if not args.no_extras and args.part == "all":
         other = "e5m2" if args.format == "e4m3" else "e4m3"
-        r2 = time_quantize(torch, R, ws, other, max(3, args.steps // 4), 1)
+        r2 = time_quantize(torch, R, ws, other, args.steps, args.warmup)
         extras[f"quantize_{other}_GBps"] = round(r2["gbps"], 1)
         extras[f"quantize_{other}_ms_per_step"] = round(r2["step_s"] * 1e3, 3)
         del ws
