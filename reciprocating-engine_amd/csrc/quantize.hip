@@ -182,6 +182,13 @@ __global__ __launch_bounds__(64 * WAVES) void quantize_rows_fast(QBatch B, int s
             if (row == 0 && M.exp_bias)
                 *M.exp_bias = fixed_bias ? fixed_bias[mi] : (uint32_t)Fp8<F>::BIAS;
         }
+        // The next row's loads go out before this row's encode and stores.
+        u32x4 vn[VPT];
+        const bool more = g + G < B.total_rows;
+        if (more) {
+            locate(g + G, mi);
+            load(row_src(g + G, mi), (int)(B.m[mi].cols / EPV), vn);
+        }
 
         // Phase 2: codes from registers. q = RN32(x * RN64(1/s)) equals the
         // IEEE f32 quotient RN32(x / s) for every finite x and every finite
@@ -231,9 +238,9 @@ __global__ __launch_bounds__(64 * WAVES) void quantize_rows_fast(QBatch B, int s
             }
         }
 
-        if (g + G < B.total_rows) {
-            locate(g + G, mi);
-            load(row_src(g + G, mi), (int)(B.m[mi].cols / EPV), v);
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) v[j] = vn[j];
         }
     }
 }
