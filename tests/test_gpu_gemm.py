@@ -1,8 +1,8 @@
 """The fused fp8-dequant GEMV / skinny GEMM and the fp8 x fp8 GEMM against the
 oracle's f32 gemm_cpu over Quantized::dequantize (fp8_probe.rs:55-78).
 
-Tolerance: relative L2 < 1e-2 over the bf16 outputs (
-the reference probe's own acceptance is 0.02, fp8_probe.rs:327,344). For the
+Tolerance: relative L2 < 1e-2 over the bf16 outputs (twice as tight as the
+reference probe's own acceptance of 0.02, fp8_probe.rs:327,344). For the
 fp8 x fp8 path the reference product uses the dequantized fp8 activation, as
 the reference probe does (fp8_probe.rs:242-248, 295-298). Exactness of the
 in-register decode is checked on its own: a one-hot activation reads every
