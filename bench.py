@@ -254,7 +254,21 @@ def bench_fp8_gemm(torch, R, gen, M, N, K):
             "mfma_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value}
 
 
-def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048):
+def cpu_f32_quantize(x_host, rows, cols):
+    """The oracle's quantize_with (reng-fp8's algorithm, <= 8 threads by its
+    split rule) on one f32 matrix: microseconds, the median of 5."""
+    import oracle as O
+
+    O.quantize_with(x_host, rows, cols, "e4m3", "pcs", 1.0)
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        O.quantize_with(x_host, rows, cols, "e4m3", "pcs", 1.0)
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[2] * 1e6
+
+
+def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048, cpu=False):
     copies = 32
     mats = []
     for _ in range(copies):
@@ -266,8 +280,14 @@ def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048):
     secs = graph_time(torch, lambda i: R.quantize_into(mats[i % copies][0], rows, cols, "e4m3", "pcs", 1.0,
                                                        mats[i % copies][1], mats[i % copies][2]), 2 * copies)
     nbytes = quant_bytes(rows, cols, 4)
-    return {"rows": rows, "cols": cols, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
-            "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "rotated_copies": copies}
+    rec = {"rows": rows, "cols": cols, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
+           "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "rotated_copies": copies}
+    if cpu:
+        us = cpu_f32_quantize(mats[0][0].cpu().numpy(), rows, cols)
+        threads = max(1, min(8, (rows * cols) >> 20, rows))   # reng-fp8's split rule
+        rec["cpu_baseline"] = {"us": round(us, 1), "GBps": round(nbytes / us / 1e3, 2), "threads": threads,
+                               "kind": "port", "sample": "the first of the rotated matrices"}
+    return rec
 
 
 def bench_decode_step(layers=4, positions=512):
@@ -409,7 +429,7 @@ def main():
             if not args.no_cpu:
                 out[0]["cpu_baseline"] = decode_cpu_record()
         else:
-            out = [bench_f32_quantize(torch, R, gen)]
+            out = [bench_f32_quantize(torch, R, gen, cpu=not args.no_cpu)]
         log(json.dumps(out))
         return
     t0 = time.perf_counter()
@@ -448,7 +468,7 @@ def main():
         torch.cuda.empty_cache()
         gen = torch.Generator(device="cuda")
         gen.manual_seed(99)
-        extras["f32_2048x2048_quantize"] = bench_f32_quantize(torch, R, gen)
+        extras["f32_2048x2048_quantize"] = bench_f32_quantize(torch, R, gen, cpu=not args.no_cpu)
         extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096),
                                      bench_w8a16(torch, R, gen, 1, 4096, 14336)]
         log("gemv b1:", extras["gemv_b1_llama8b"])
