@@ -170,11 +170,13 @@ RENG_HIP_API int reng_hip_gemm_fp8_scaled(const uint8_t *a, int a_format, const 
  *
  * The reference's fp8 load path stops at a refusal where the quantized codes
  * would meet a device layer (layer_views, crates/reng-model/src/lib.rs:2636-2649);
- * these entry points are the non-GEMM steps of that layer, one token per call,
- * with the semantics of its CPU decoder layer (layer_cpu, causal, Llama form:
- * crates/reng-synapse/src/model.rs:2903-3100). The seven projections are
- * reng_hip_gemm_w8a16 with M = 1 on the layer's codes and scales. Residual
- * stream f32; GEMV inputs bf16; caches bf16 [positions, n_kv_heads * head_dim].
+ * these entry points are the steps of that layer, one token per call, with the
+ * semantics of its CPU decoder layer (layer_cpu, causal, Llama form:
+ * crates/reng-synapse/src/model.rs:2903-3100). The seven projections are the
+ * GEMV (reng_hip_gemm_w8a16, M = 1) on the layer's codes and scales, or its
+ * fused forms below, which take the neighbouring steps into the same pass and
+ * are bit-identical to the chain of separate calls. Residual stream f32; GEMV
+ * inputs bf16; caches bf16 [positions, n_kv_heads * head_dim].
  * ------------------------------------------------------------------------- */
 
 /* Longest cache an attention call reads: 128Ki rows, Llama 3.1's context. */
