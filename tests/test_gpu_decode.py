@@ -496,6 +496,8 @@ def test_attention_forms_against_numpy(nh, nkv, hd):
     bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
     scale = hd ** -0.5
     lengths = (1, 33, 255, 256, 257, 512, 513, 700, 5000, 20000) if hd <= 128 else (1, 33, 700)
+    if (nh, nkv) == (16, 1):
+        lengths += (131072,)   # the longest cache: 64 splits of 2048 rows (eight tiles each)
     ws = torch.full((R.attention_workspace_bytes(nh, hd, max(lengths)) // 4 + 1,), float("nan"),
                     dtype=torch.float32, device="cuda")
     for length in lengths:
