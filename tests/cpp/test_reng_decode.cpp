@@ -67,6 +67,14 @@ int refusals(const std::string &dir) {
     expect_error("too many positions", [&] { Fp8Decoder d(cfg, w, RENG_HIP_ATTENTION_MAX_LEN + 1); },
                  "max_positions");
     expect_error("fp8 layers do not match", [&] { Fp8Decoder d(cfg, w, 8); }, "fp8 layers do not match");
+    // A hidden row past the GEMV's LDS stage (checked before any shape or device work).
+    LlamaWeights wide = plain;
+    wide.fp8.emplace(plain.layers.size());
+    expect_error("hidden_size past 32768", [&] {
+        LlamaConfig c = cfg;
+        c.hidden_size = 40960;
+        Fp8Decoder d(c, wide, 8);
+    }, "hidden_size 40960");
     std::printf("%d failed\n", failures);
     return failures ? 1 : 0;
 }
