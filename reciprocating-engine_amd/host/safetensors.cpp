@@ -230,9 +230,18 @@ void Checkpoint::add_file(const std::string &path, const std::map<std::string, b
         if (ti.begin > ti.end || ti.end > data_len)
             throw Error("safetensors: " + fname + ": tensor " + kv.first + ": data outside the file");
         if (ti.dtype != Dtype::Other) {
-            size_t n = 1;
-            for (size_t d : ti.shape) n *= d;
-            if (n * dtype_size(ti.dtype) != ti.end - ti.begin)
+            // The element count and its byte size are checked for overflow: a
+            // shape whose product wraps could otherwise match the byte range
+            // (even 0) while consumers trust the shape.
+            size_t n = 1, nbytes = 0;
+            for (size_t d : ti.shape)
+                if (__builtin_mul_overflow(n, d, &n))
+                    throw Error("safetensors: " + fname + ": tensor " + kv.first + ": shape " + shape_str(ti.shape) +
+                                " overflows");
+            if (__builtin_mul_overflow(n, dtype_size(ti.dtype), &nbytes))
+                throw Error("safetensors: " + fname + ": tensor " + kv.first + ": shape " + shape_str(ti.shape) +
+                            " overflows");
+            if (nbytes != ti.end - ti.begin)
                 throw Error("safetensors: " + fname + ": tensor " + kv.first + ": " + std::to_string(ti.end - ti.begin) +
                             " bytes for " + ti.dtype_name + " " + shape_str(ti.shape));
         }

@@ -129,12 +129,29 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _dev(t, what):
+def _dev(t, what, nbytes=None):
+    """The device address of a contiguous GPU tensor; with nbytes, refuse a
+    tensor smaller than the bytes the C call will touch (the reference refuses
+    a weight slice of the wrong length, crates/reng-fp8/src/lib.rs:528; here a
+    short buffer would be read or written past its end on the device)."""
     if not t.is_cuda:
         raise ValueError(f"{what} must be a GPU tensor")
     if not t.is_contiguous():
         raise ValueError(f"{what} must be contiguous")
+    if nbytes is not None:
+        have = t.numel() * t.element_size()
+        if have < nbytes:
+            raise ValueError(f"{what} length against the shape: {have} bytes, the call touches {nbytes}")
     return ctypes.c_void_p(t.data_ptr())
+
+
+def _opt(t, what, nbytes=None):
+    return None if t is None else _dev(t, what, nbytes)
+
+
+def _span(rows, cols, ld):
+    """Elements a [rows, cols] window of row pitch ld spans."""
+    return 0 if rows == 0 or cols == 0 else (rows - 1) * ld + cols
 
 
 def _dtype_code(t):
@@ -180,7 +197,8 @@ class Quantized:
         import torch
 
         out = torch.empty(self.rows * self.cols, dtype=torch.float32, device=self.codes.device)
-        _check(lib().reng_hip_dequantize(_dev(self.codes, "codes"), _dev(self.scales, "scales"), self.rows,
+        _check(lib().reng_hip_dequantize(_dev(self.codes, "codes", self.rows * self.cols),
+                                         _dev(self.scales, "scales", 4 * self.rows), self.rows,
                                          self.cols, _fmt(self.format), F32, _dev(out, "out"), _stream()))
         return out
 
@@ -188,17 +206,20 @@ class Quantized:
         import torch
 
         out = torch.empty(self.rows * self.cols, dtype=torch.int16, device=self.codes.device)
-        _check(lib().reng_hip_dequantize(_dev(self.codes, "codes"), _dev(self.scales, "scales"), self.rows,
+        _check(lib().reng_hip_dequantize(_dev(self.codes, "codes", self.rows * self.cols),
+                                         _dev(self.scales, "scales", 4 * self.rows), self.rows,
                                          self.cols, _fmt(self.format), BF16, _dev(out, "out"), _stream()))
         return out
 
 
 def quantize_into(w, rows, cols, fmt, scaling, backoff, codes, scales, exp_bias=None, ld=None):
     """Device quantize into caller-owned tensors (no allocation)."""
-    _check(lib().reng_hip_quantize(_dev(w, "w"), _dtype_code(w), rows, cols, cols if ld is None else ld,
-                                   _fmt(fmt), _sc(scaling), float(backoff), _dev(codes, "codes"),
-                                   _dev(scales, "scales"),
-                                   None if exp_bias is None else _dev(exp_bias, "exp_bias"), _stream()))
+    ld = cols if ld is None else ld
+    dt = _dtype_code(w)
+    _check(lib().reng_hip_quantize(_dev(w, "weight", _span(rows, cols, ld) * (2 if dt == BF16 else 4)), dt, rows,
+                                   cols, ld, _fmt(fmt), _sc(scaling), float(backoff),
+                                   _dev(codes, "codes", rows * cols), _dev(scales, "scales", 4 * rows),
+                                   _opt(exp_bias, "exp_bias", 4), _stream()))
 
 
 def quantize_with(w, rows, cols, fmt, scaling, backoff=DEFAULT_BACKOFF, ld=None):
@@ -225,6 +246,8 @@ def quantize_host(w, rows, cols, fmt, scaling, backoff=DEFAULT_BACKOFF):
     dt = BF16 if w.dtype == np.uint16 else F32 if w.dtype == np.float32 else None
     if dt is None:
         raise ValueError(f"weights must be uint16 (bf16 bits) or float32, not {w.dtype}")
+    if rows > 0 and cols > 0 and w.size != rows * cols:   # lib.rs:528 (an empty shape is the library's refusal)
+        raise ValueError(f"weight length against the shape: {w.size} elements for [{rows}, {cols}]")
     codes = np.empty(rows * cols, dtype=np.uint8)
     scales = np.empty(rows, dtype=np.float32)
     eb = ctypes.c_uint32(0)
@@ -234,12 +257,21 @@ def quantize_host(w, rows, cols, fmt, scaling, backoff=DEFAULT_BACKOFF):
     return codes, scales, int(eb.value)
 
 
-def quantize_batch(mats, fmt, scaling, backoff=DEFAULT_BACKOFF, dtype=BF16):
-    """mats: list of (w, rows, cols, codes, scales, exp_bias_or_None) device tensors."""
+def quantize_batch(mats, fmt, scaling, backoff=DEFAULT_BACKOFF):
+    """mats: list of (w, rows, cols, codes, scales, exp_bias_or_None) device
+    tensors, all bf16 (or its int16 bits) or all f32."""
+    if not mats:
+        raise ValueError("empty batch")
+    dts = {_dtype_code(m[0]) for m in mats}
+    if len(dts) != 1:
+        raise ValueError("a batch holds one weight dtype (bf16 or f32), not a mix")
+    dtype = dts.pop()
+    esz = 2 if dtype == BF16 else 4
     arr = (_Matrix * len(mats))()
     for i, (w, rows, cols, codes, scales, eb) in enumerate(mats):
-        arr[i] = _Matrix(w.data_ptr(), codes.data_ptr(), scales.data_ptr(),
-                         0 if eb is None else eb.data_ptr(), rows, cols, cols)
+        arr[i] = _Matrix(_dev(w, f"weight {i}", rows * cols * esz).value, _dev(codes, f"codes {i}", rows * cols).value,
+                         _dev(scales, f"scales {i}", 4 * rows).value,
+                         0 if eb is None else _dev(eb, f"exp_bias {i}", 4).value, rows, cols, cols)
     _check(lib().reng_hip_quantize_batch(arr, len(mats), dtype, _fmt(fmt), _sc(scaling), float(backoff),
                                          _stream()))
 
@@ -248,8 +280,10 @@ def row_absmax(w, rows, cols, ld=None):
     import torch
 
     out = torch.empty(rows, dtype=torch.float32, device=w.device)
-    _check(lib().reng_hip_row_absmax(_dev(w, "w"), _dtype_code(w), rows, cols, cols if ld is None else ld,
-                                     _dev(out, "out"), _stream()))
+    ld = cols if ld is None else ld
+    dt = _dtype_code(w)
+    _check(lib().reng_hip_row_absmax(_dev(w, "weight", _span(rows, cols, ld) * (2 if dt == BF16 else 4)), dt, rows,
+                                     cols, ld, _dev(out, "out"), _stream()))
     return out
 
 
@@ -278,7 +312,8 @@ def _errors(w, q, max_rows):
     k = -(-q.rows // step)
     mean = torch.empty(k, dtype=torch.float32, device=q.codes.device)
     mx = torch.empty(k, dtype=torch.float32, device=q.codes.device)
-    _check(lib().reng_hip_row_errors(_dev(w, "w"), _dev(q.codes, "codes"), _dev(q.scales, "scales"), q.rows,
+    _check(lib().reng_hip_row_errors(_dev(w, "weight", 2 * q.rows * q.cols), _dev(q.codes, "codes", q.rows * q.cols),
+                                     _dev(q.scales, "scales", 4 * q.rows), q.rows,
                                      q.cols, _fmt(q.format), max_rows, _dev(mean, "mean"), _dev(mx, "max"),
                                      _stream()))
     return mean, mx
@@ -300,9 +335,9 @@ def gemm_w8a16(x, codes, scales, M, N, K, fmt, y=None):
 
     if y is None:
         y = torch.empty(M * N, dtype=torch.bfloat16, device=x.device)
-    _check(lib().reng_hip_gemm_w8a16(_dev(x, "x"), _dev(codes, "codes"),
-                                     None if scales is None else _dev(scales, "scales"), M, N, K, _fmt(fmt),
-                                     _dev(y, "y"), _stream()))
+    _check(lib().reng_hip_gemm_w8a16(_dev(x, "x", 2 * M * K), _dev(codes, "codes", N * K),
+                                     _opt(scales, "scales", 4 * N), M, N, K, _fmt(fmt),
+                                     _dev(y, "y", 2 * M * N), _stream()))
     return y
 
 
@@ -314,10 +349,9 @@ def gemm_fp8_scaled(a, a_fmt, scale_a, b, b_fmt, scale_b, M, N, K, out=None):
         out = torch.empty(M * N, dtype=torch.bfloat16, device=a.device)
     na = 0 if scale_a is None else scale_a.numel()
     nb = 0 if scale_b is None else scale_b.numel()
-    _check(lib().reng_hip_gemm_fp8_scaled(_dev(a, "a"), _fmt(a_fmt), None if scale_a is None else _dev(scale_a, "sa"),
-                                          na, _dev(b, "b"), _fmt(b_fmt),
-                                          None if scale_b is None else _dev(scale_b, "sb"), nb, M, N, K,
-                                          _dev(out, "out"), _stream()))
+    _check(lib().reng_hip_gemm_fp8_scaled(_dev(a, "a", M * K), _fmt(a_fmt), _opt(scale_a, "scale_a", 4 * na),
+                                          na, _dev(b, "b", N * K), _fmt(b_fmt), _opt(scale_b, "scale_b", 4 * nb), nb,
+                                          M, N, K, _dev(out, "out", 2 * M * N), _stream()))
     return out
 
 
@@ -332,8 +366,8 @@ def rms_norm_bf16(x, gamma, rows, cols, eps, out=None):
 
     if out is None:
         out = torch.empty(rows * cols, dtype=torch.bfloat16, device=x.device)
-    _check(lib().reng_hip_rms_norm_bf16(_dev(x, "x"), _dev(gamma, "gamma"), rows, cols, eps, _dev(out, "out"),
-                                        _stream()))
+    _check(lib().reng_hip_rms_norm_bf16(_dev(x, "x", 4 * rows * cols), _dev(gamma, "gamma", 4 * cols), rows, cols,
+                                        eps, _dev(out, "out", 2 * rows * cols), _stream()))
     return out
 
 
@@ -343,9 +377,9 @@ def gemv_residual(x, codes, scales, n, k, fmt, residual, out=None):
 
     if out is None:
         out = torch.empty(n, dtype=torch.float32, device=x.device)
-    _check(lib().reng_hip_gemv_w8a16_residual(_dev(x, "x"), _dev(codes, "codes"),
-                                              None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt),
-                                              _dev(residual, "residual"), _dev(out, "out"), _stream()))
+    _check(lib().reng_hip_gemv_w8a16_residual(_dev(x, "x", 2 * k), _dev(codes, "codes", n * k),
+                                              _opt(scales, "scales", 4 * n), n, k, _fmt(fmt),
+                                              _dev(residual, "residual", 4 * n), _dev(out, "out", 4 * n), _stream()))
     return out
 
 
@@ -356,9 +390,9 @@ def gemv_swiglu(x, codes, scales, n, k, fmt, out=None):
 
     if out is None:
         out = torch.empty(n // 2, dtype=torch.bfloat16, device=x.device)
-    _check(lib().reng_hip_gemv_w8a16_swiglu(_dev(x, "x"), _dev(codes, "codes"),
-                                            None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt),
-                                            _dev(out, "out"), _stream()))
+    _check(lib().reng_hip_gemv_w8a16_swiglu(_dev(x, "x", 2 * k), _dev(codes, "codes", n * k),
+                                            _opt(scales, "scales", 4 * n), n, k, _fmt(fmt),
+                                            _dev(out, "out", 2 * (n // 2)), _stream()))
     return out
 
 
@@ -370,8 +404,9 @@ def gemv_rmsnorm(x, gamma, eps, codes, scales, n, k, fmt, swiglu=False, out=None
     if out is None:
         out = torch.empty(n // 2 if swiglu else n, dtype=torch.bfloat16, device=x.device)
     fn = lib().reng_hip_gemv_w8a16_rmsnorm_swiglu if swiglu else lib().reng_hip_gemv_w8a16_rmsnorm
-    _check(fn(_dev(x, "x"), _dev(gamma, "gamma"), eps, _dev(codes, "codes"),
-              None if scales is None else _dev(scales, "scales"), n, k, _fmt(fmt), _dev(out, "out"), _stream()))
+    _check(fn(_dev(x, "x", 4 * k), _dev(gamma, "gamma", 4 * k), eps, _dev(codes, "codes", n * k),
+              _opt(scales, "scales", 4 * n), n, k, _fmt(fmt), _dev(out, "out", 2 * (n // 2 if swiglu else n)),
+              _stream()))
     return out
 
 
@@ -394,11 +429,13 @@ def gemv_rmsnorm_qkv_rope(x, gamma, eps, codes, scales, n_heads, n_kv_heads, hea
                           q, k_row, v_row):
     """Norm + [q | k | v] projection + RoPE + cache-row writes in one pass over
     codes in qkv_rope_row_order."""
+    n = (n_heads + 2 * n_kv_heads) * head_dim
     _check(lib().reng_hip_gemv_w8a16_rmsnorm_qkv_rope(
-        _dev(x, "x"), _dev(gamma, "gamma"), eps, _dev(codes, "codes"),
-        None if scales is None else _dev(scales, "scales"), n_heads, n_kv_heads, head_dim, k, _fmt(fmt),
-        _dev(sin_row, "sin_row"), _dev(cos_row, "cos_row"), _dev(q, "q"), _dev(k_row, "k_row"),
-        _dev(v_row, "v_row"), _stream()))
+        _dev(x, "x", 4 * k), _dev(gamma, "gamma", 4 * k), eps, _dev(codes, "codes", n * k),
+        _opt(scales, "scales", 4 * n), n_heads, n_kv_heads, head_dim, k, _fmt(fmt),
+        _dev(sin_row, "sin_row", 4 * head_dim), _dev(cos_row, "cos_row", 4 * head_dim),
+        _dev(q, "q", 2 * n_heads * head_dim), _dev(k_row, "k_row", 2 * n_kv_heads * head_dim),
+        _dev(v_row, "v_row", 2 * n_kv_heads * head_dim), _stream()))
 
 
 def add_rms_norm_bf16(x, d, gamma, rows, cols, eps, h=None, out=None):
@@ -409,16 +446,20 @@ def add_rms_norm_bf16(x, d, gamma, rows, cols, eps, h=None, out=None):
         h = torch.empty(rows * cols, dtype=torch.float32, device=x.device)
     if out is None:
         out = torch.empty(rows * cols, dtype=torch.bfloat16, device=x.device)
-    _check(lib().reng_hip_add_rms_norm_bf16(_dev(x, "x"), _dev(d, "d"), _dev(gamma, "gamma"), rows, cols, eps,
-                                            _dev(h, "h"), _dev(out, "out"), _stream()))
+    n = rows * cols
+    _check(lib().reng_hip_add_rms_norm_bf16(_dev(x, "x", 4 * n), _dev(d, "d", 2 * n), _dev(gamma, "gamma", 4 * cols),
+                                            rows, cols, eps, _dev(h, "h", 4 * n), _dev(out, "out", 2 * n),
+                                            _stream()))
     return h, out
 
 
 def rope_append(q, k, v, n_heads, n_kv_heads, head_dim, sin_row, cos_row, k_row, v_row):
     """Rotate-half RoPE of one position: q in place, k into k_row, v copied to v_row."""
-    _check(lib().reng_hip_rope_append(_dev(q, "q"), _dev(k, "k"), _dev(v, "v"), n_heads, n_kv_heads, head_dim,
-                                      _dev(sin_row, "sin_row"), _dev(cos_row, "cos_row"), _dev(k_row, "k_row"),
-                                      _dev(v_row, "v_row"), _stream()))
+    nq, nk = 2 * n_heads * head_dim, 2 * n_kv_heads * head_dim
+    _check(lib().reng_hip_rope_append(_dev(q, "q", nq), _dev(k, "k", nk), _dev(v, "v", nk), n_heads, n_kv_heads,
+                                      head_dim, _dev(sin_row, "sin_row", 4 * head_dim),
+                                      _dev(cos_row, "cos_row", 4 * head_dim), _dev(k_row, "k_row", nk),
+                                      _dev(v_row, "v_row", nk), _stream()))
 
 
 def attention_decode(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, length, scale, out=None):
@@ -427,8 +468,10 @@ def attention_decode(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, length,
 
     if out is None:
         out = torch.empty(n_heads * head_dim, dtype=torch.bfloat16, device=q.device)
-    _check(lib().reng_hip_attention_decode(_dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), n_heads,
-                                           n_kv_heads, head_dim, length, scale, _dev(out, "out"), _stream()))
+    nq, nc = 2 * n_heads * head_dim, 2 * length * n_kv_heads * head_dim
+    _check(lib().reng_hip_attention_decode(_dev(q, "q", nq), _dev(k_cache, "k_cache", nc),
+                                           _dev(v_cache, "v_cache", nc), n_heads, n_kv_heads, head_dim, length, scale,
+                                           _dev(out, "out", nq), _stream()))
     return out
 
 
@@ -449,11 +492,13 @@ def attention_decode_split(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, l
     if workspace is None:
         workspace = torch.empty(max(1, attention_workspace_bytes(n_heads, head_dim, length)), dtype=torch.uint8,
                                 device=q.device)
-    _check(lib().reng_hip_attention_decode_split(_dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"),
-                                                 n_heads, n_kv_heads, head_dim, length, scale,
+    nq, nc = 2 * n_heads * head_dim, 2 * length * n_kv_heads * head_dim
+    _check(lib().reng_hip_attention_decode_split(_dev(q, "q", nq), _dev(k_cache, "k_cache", nc),
+                                                 _dev(v_cache, "v_cache", nc), n_heads, n_kv_heads, head_dim, length,
+                                                 scale,
                                                  _dev(workspace, "workspace"),
-                                                 workspace.numel() * workspace.element_size(), _dev(out, "out"),
-                                                 _stream()))
+                                                 workspace.numel() * workspace.element_size(),
+                                                 _dev(out, "out", nq), _stream()))
     return out
 
 
@@ -462,7 +507,8 @@ def silu_mul_bf16(gate, up, n, out=None):
 
     if out is None:
         out = torch.empty(n, dtype=torch.bfloat16, device=gate.device)
-    _check(lib().reng_hip_silu_mul_bf16(_dev(gate, "gate"), _dev(up, "up"), n, _dev(out, "out"), _stream()))
+    _check(lib().reng_hip_silu_mul_bf16(_dev(gate, "gate", 2 * n), _dev(up, "up", 2 * n), n, _dev(out, "out", 2 * n),
+                                        _stream()))
     return out
 
 
@@ -471,7 +517,8 @@ def add_bf16_f32(x, d, n, out=None):
 
     if out is None:
         out = torch.empty(n, dtype=torch.float32, device=x.device)
-    _check(lib().reng_hip_add_bf16_f32(_dev(x, "x"), _dev(d, "d"), n, _dev(out, "out"), _stream()))
+    _check(lib().reng_hip_add_bf16_f32(_dev(x, "x", 4 * n), _dev(d, "d", 2 * n), n, _dev(out, "out", 4 * n),
+                                       _stream()))
     return out
 
 

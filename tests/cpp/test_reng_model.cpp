@@ -297,6 +297,16 @@ void safetensors_views_convert_and_refuse() {
     write_file(d.path + "/trunc.safetensors", trunc);
     expect_throws([&] { (void)Checkpoint::open_file(d.path + "/trunc.safetensors"); }, "data outside the file",
                   "truncated");
+    // A shape whose element count wraps to 0 in 64 bits, over zero bytes; and
+    // one whose count fits but whose byte size wraps.
+    write_file(d.path + "/wrap.safetensors",
+               safetensors_bytes({{"b", "BF16", {(size_t)1 << 32, (size_t)1 << 32}, std::string()}}));
+    expect_throws([&] { (void)Checkpoint::open_file(d.path + "/wrap.safetensors"); }, "overflows",
+                  "shape product overflow");
+    write_file(d.path + "/wrapb.safetensors",
+               safetensors_bytes({{"f", "F32", {(size_t)1 << 62}, std::string()}}));
+    expect_throws([&] { (void)Checkpoint::open_file(d.path + "/wrapb.safetensors"); }, "overflows",
+                  "byte size overflow");
     std::string shorthdr(8, '\0');
     shorthdr[0] = (char)200;
     write_file(d.path + "/short.safetensors", shorthdr);

@@ -146,3 +146,73 @@ def probe_activations(n):
     """fp8_probe.rs:46-50."""
     i = np.arange(n, dtype=np.int64)
     return (((i * 7919) % 2003).astype(np.float32) - np.float32(1000.0)) / np.float32(700.0)
+
+
+def special_matrix_f32(rng, rows=24, cols=512):
+    """f32 weights (the [2048, 2048] workload's input type): N(0, 0.02) rows with
+    0.1% of entries x50, then rows that exercise every special case of the f32
+    entry: +-inf and NaN of both signs inside per-channel rows, a row whose
+    absmax is 2^-149 (so s = m / 240 underflows to 0: x / 0 saturates and
+    0 / 0 is x86's negative default NaN), rows whose s is subnormal (normal and
+    subnormal entries), an all-NaN row (absmax 0, s = 1), rows of zeros and of
+    negative zeros, f32 max and out-of-range finite values, and the tie
+    240 * 2^-150 (m = 120 * 2^-149) where s rounds to 0 by ties-to-even next to
+    m = 121 * 2^-149 where it rounds up to 2^-149."""
+    assert rows >= 24 and cols >= 16
+    x = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    out = rng.random((rows, cols)) < 0.001
+    x[out] *= np.float32(50.0)
+    tiny = np.float32(2.0 ** -149)
+    x[1, 5] = np.inf
+    x[2, 7] = -np.inf
+    x[3, 11] = np.array(0x7FC00001, dtype=np.uint32).view(np.float32)      # +NaN with a payload
+    x[4, 0] = np.array(0xFFC00000, dtype=np.uint32).view(np.float32)       # -NaN
+    x[4, 3] = np.inf                                                       # and +inf in the same row
+    x[5] = rng.choice(np.array([0.0, -0.0, tiny, -tiny], dtype=np.float32), cols)
+    x[5, 0] = tiny                                                         # absmax 2^-149: s = 0
+    x[6] = (rng.standard_normal(cols) * 1e-37).astype(np.float32)          # s ~ 4e-40, subnormal
+    x[7] = (rng.standard_normal(cols) * 1e-40).astype(np.float32)          # subnormal entries, subnormal s
+    x[8] = 0.0
+    x[9] = -0.0
+    x[10] = np.array(0x7FC00000, dtype=np.uint32).view(np.float32)         # all NaN: absmax 0, s = 1
+    x[10, ::3] = np.array(0xFFC00000, dtype=np.uint32).view(np.float32)
+    x[11, :4] = np.float32(3.4028235e38)                                   # f32 max
+    x[11, 4:8] = np.float32(-3.4028235e38)
+    x[12, ::5] = np.float32(3e38)
+    x[13] = rng.integers(-120, 121, cols).astype(np.float32) * tiny
+    x[13, 0] = 120 * tiny                                                  # m / 240 = 2^-150: ties to 0
+    x[14] = rng.integers(-121, 122, cols).astype(np.float32) * tiny
+    x[14, 0] = 121 * tiny                                                  # m / 240 rounds up to 2^-149
+    x[15] = rng.integers(-1000, 1001, cols).astype(np.float32) * tiny      # s = 1000 * 2^-149 / 240
+    x[15, 0] = 1000 * tiny
+    x[16, 1] = -np.inf
+    x[16, 2] = np.inf
+    return x
+
+
+def quantize_f32_closed_form(x, fmt, scaling, backoff):
+    """What quantize_with gives f32 weights, from numpy's own f32 arithmetic
+    and the independent table search: per-channel s = RN(m / RN(max * backoff))
+    (m the NaN-ignoring row absmax, 1 for m = 0), hw s = 2^(bias - b) for the
+    largest allowed b whose range covers RN(tensor absmax / backoff), unit
+    s = 1; codes = nearest_encode(RN(x / s))."""
+    rows, cols = x.shape
+    maxf = np.float32(240.0 if fmt == E4M3 else 57344.0)
+    a = np.abs(x)
+    m = np.where(np.isnan(a), np.float32(0), a).max(axis=1).astype(np.float32)
+    bias = BIAS[fmt]
+    if scaling == "pcs":
+        full = np.float32(maxf * np.float32(backoff))
+        with np.errstate(all="ignore"):
+            s = np.where(m > 0, m / full, np.float32(1.0)).astype(np.float32)
+    elif scaling == "hw":
+        with np.errstate(all="ignore"):
+            tm = np.float32(m.max() / np.float32(backoff))
+        allowed = [15, 11, 7, 3] if fmt == E4M3 else [15]
+        bias = next((bb for bb in allowed if tm <= maxf * np.float32(2.0 ** (BIAS[fmt] - bb))), allowed[-1])
+        s = np.full(rows, np.float32(2.0 ** (BIAS[fmt] - bias)), dtype=np.float32)
+    else:
+        s = np.ones(rows, dtype=np.float32)
+    with np.errstate(all="ignore"):
+        quot = (x / s[:, None]).astype(np.float32)
+    return nearest_encode(quot, fmt), s, bias

@@ -82,3 +82,95 @@ def test_the_binding_rejects_unknown_names():
         R._sc("bogus")
     assert R._fmt("HF8") == R.E4M3 and R._fmt("f8") == R.E5M2
     assert R._sc("per-channel") == R.PCS and R._sc("none") == R.UNIT
+
+
+class _FakeDev:
+    """Stands in for a GPU tensor in the binding's argument checks, which run
+    before any library call (a check that passed would hand the library this
+    address, so every case below must be refused)."""
+
+    def __init__(self, nbytes, dtype=None):
+        import torch
+
+        self.dtype = torch.uint8 if dtype is None else dtype
+        self._n = nbytes // torch.empty(0, dtype=self.dtype).element_size()
+        self.is_cuda = True
+        self.device = torch.device("cpu")   # where a wrapper allocates its outputs (never reached)
+
+    def is_contiguous(self):
+        return True
+
+    def numel(self):
+        return self._n
+
+    def element_size(self):
+        import torch
+
+        return torch.empty(0, dtype=self.dtype).element_size()
+
+    def data_ptr(self):
+        return 16
+
+
+def test_the_binding_refuses_short_buffers():
+    import numpy as np
+    import torch
+
+    bf, f32 = torch.bfloat16, torch.float32
+    rows, cols = 8, 64
+    codes, scales = _FakeDev(rows * cols), _FakeDev(4 * rows, f32)
+    with pytest.raises(ValueError, match="weight length against the shape"):
+        R.quantize_into(_FakeDev(2 * rows * cols - 2, bf), rows, cols, "e4m3", "pcs", 1.0, codes, scales)
+    with pytest.raises(ValueError, match="weight length"):   # a row pitch widens the span
+        R.quantize_into(_FakeDev(2 * rows * cols, bf), rows, cols, "e4m3", "pcs", 1.0, codes, scales, ld=72)
+    with pytest.raises(ValueError, match="weight length"):   # f32 weights: 4 bytes an element
+        R.quantize_into(_FakeDev(2 * rows * cols, f32), rows, cols, "e4m3", "pcs", 1.0, codes, scales)
+    with pytest.raises(ValueError, match="codes length"):
+        R.quantize_into(_FakeDev(2 * rows * cols, bf), rows, cols, "e4m3", "pcs", 1.0, _FakeDev(rows * cols - 1),
+                        scales)
+    with pytest.raises(ValueError, match="scales length"):
+        R.quantize_into(_FakeDev(2 * rows * cols, bf), rows, cols, "e4m3", "pcs", 1.0, codes, _FakeDev(4 * rows - 4, f32))
+    with pytest.raises(ValueError, match="exp_bias length"):
+        R.quantize_into(_FakeDev(2 * rows * cols, bf), rows, cols, "e4m3", "pcs", 1.0, codes, scales, _FakeDev(2))
+    with pytest.raises(ValueError, match="weight length"):
+        R.row_absmax(_FakeDev(2 * rows * cols - 2, bf), rows, cols)
+    # quantize_batch: the dtype comes from the tensors, one dtype a batch.
+    good = (_FakeDev(2 * rows * cols, bf), rows, cols, codes, scales, None)
+    with pytest.raises(ValueError, match="one weight dtype"):
+        R.quantize_batch([good, (_FakeDev(4 * rows * cols, f32), rows, cols, codes, scales, None)], "e4m3", "pcs")
+    with pytest.raises(ValueError, match="weight 1 length"):
+        R.quantize_batch([good, (_FakeDev(2 * rows * cols, f32), rows, cols, codes, scales, None)][:1] +
+                         [(_FakeDev(2 * rows * cols - 2, bf), rows, cols, codes, scales, None)], "e4m3", "pcs")
+    with pytest.raises(ValueError, match="empty batch"):
+        R.quantize_batch([], "e4m3", "pcs")
+    # The consumer.
+    M, N, K = 4, 32, 128
+    x, c, s, y = _FakeDev(2 * M * K, bf), _FakeDev(N * K), _FakeDev(4 * N, f32), _FakeDev(2 * M * N, bf)
+    for args, what in [((_FakeDev(2 * M * K - 2, bf), c, s), "x"), ((x, _FakeDev(N * K - 1), s), "codes"),
+                       ((x, c, _FakeDev(4 * N - 4, f32)), "scales")]:
+        with pytest.raises(ValueError, match=f"{what} length"):
+            R.gemm_w8a16(*args, M, N, K, "e4m3", y)
+    with pytest.raises(ValueError, match="y length"):
+        R.gemm_w8a16(x, c, s, M, N, K, "e4m3", _FakeDev(2 * M * N - 2, bf))
+    a = _FakeDev(M * K)
+    with pytest.raises(ValueError, match="b length"):
+        R.gemm_fp8_scaled(a, "e4m3", None, _FakeDev(N * K - 1), "e4m3", None, M, N, K, y)
+    with pytest.raises(ValueError, match="out length"):
+        R.gemm_fp8_scaled(a, "e4m3", None, c, "e4m3", None, M, N, K, _FakeDev(2 * M * N - 2, bf))
+    # The host entry: the reference's own refusal of a wrong-length slice.
+    with pytest.raises(ValueError, match="weight length against the shape"):
+        R.quantize_host(np.zeros(rows * cols - 1, dtype=np.uint16), rows, cols, "e4m3", "pcs")
+    with pytest.raises(ValueError, match="weight length against the shape"):
+        R.quantize_host(np.zeros(rows * cols + 1, dtype=np.float32), rows, cols, "e4m3", "pcs")
+    # The decode-step helpers.
+    with pytest.raises(ValueError, match="residual length"):
+        R.gemv_residual(_FakeDev(2 * K, bf), c, s, N, K, "e4m3", _FakeDev(4 * N - 4, f32), _FakeDev(4 * N, f32))
+    with pytest.raises(ValueError, match="gamma length"):
+        R.rms_norm_bf16(_FakeDev(4 * rows * cols, f32), _FakeDev(4 * cols - 4, f32), rows, cols, 1e-5,
+                        _FakeDev(2 * rows * cols, bf))
+    with pytest.raises(ValueError, match="k_cache length"):
+        R.attention_decode(_FakeDev(2 * 32 * 128, bf), _FakeDev(2 * 100 * 8 * 128 - 2, bf),
+                           _FakeDev(2 * 100 * 8 * 128, bf), 32, 8, 128, 100, 0.1, _FakeDev(2 * 32 * 128, bf))
+    with pytest.raises(ValueError, match="v_row length"):
+        R.rope_append(_FakeDev(2 * 4 * 64, bf), _FakeDev(2 * 2 * 64, bf), _FakeDev(2 * 2 * 64, bf), 4, 2, 64,
+                      _FakeDev(4 * 64, f32), _FakeDev(4 * 64, f32), _FakeDev(2 * 2 * 64, bf), _FakeDev(2 * 64, bf))

@@ -321,3 +321,33 @@ def test_row_absmax_dequantize_and_error_sampling(R):
     for a in (0.5, 0.9375, 1.0, 15.0, 16.0, 1000.0, 1e9):
         assert R.choose_exp_bias(a, E4M3) == O.choose_exp_bias(a, E4M3)
     assert R.choose_exp_bias(1e9, E5M2) == 15
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+@pytest.mark.parametrize("scaling", ["pcs", "hw", "unit"])
+def test_f32_special_values_inside_rows(R, fmt, scaling):
+    """f32 input with +-inf and NaN inside rows, s underflowing to 0, subnormal
+    s, all-NaN and zero rows (helpers.special_matrix_f32), at the widths of the
+    f32 exact-fit kernels (2048, 8192), a predicated width and the generic one."""
+    from helpers import special_matrix_f32
+
+    rng = np.random.default_rng(53 + fmt)
+    for rows, cols in [(24, 2048), (40, 8192), (24, 4096), (24, 520), (30, 100)]:
+        x = special_matrix_f32(rng, rows, cols)
+        for backoff in (1.0, 0.5, 2.0):
+            check_quantize(R, x.ravel(), rows, cols, fmt, scaling, backoff,
+                           label=f"f32 {rows}x{cols} {scaling} b{backoff}")
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_the_f32_2048x2048_workload(R, fmt):
+    """The reference's CPU-runnable case at its full size: one f32 [2048, 2048]
+    matrix, N(0, 0.02) with 0.1% of entries (4194, drawn without replacement)
+    x50, per-channel scales, backoff 1; and the same matrix under hw and unit."""
+    rng = np.random.default_rng(2048)
+    rows = cols = 2048
+    x = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32).ravel()
+    idx = rng.choice(rows * cols, 4194, replace=False)
+    x[idx] *= np.float32(50.0)
+    for sc in ("pcs", "hw", "unit"):
+        check_quantize(R, x, rows, cols, fmt, sc, label=f"f32 2048x2048 {sc}")

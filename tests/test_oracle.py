@@ -399,3 +399,65 @@ def test_gemm_and_rel_l2_follow_numpy():
     g = c + np.float32(0.01)
     want = np.sqrt(np.sum((g - c).astype(np.float64) ** 2)) / np.sqrt(np.sum(c.astype(np.float64) ** 2))
     assert abs(O.rel_l2(g, c) - want) <= 1e-6 * want
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_f32_quantize_follows_numpy_division_and_the_table_search(fmt):
+    """orc_quantize_f32_with, the checker of the f32 [2048, 2048] workload,
+    against numpy's f32 arithmetic and the nearest-value search, on every
+    special case of f32 input (helpers.special_matrix_f32), for the three
+    schemes and backoffs below, above and at 1."""
+    from helpers import quantize_f32_closed_form, special_matrix_f32
+
+    rng = np.random.default_rng(41 + fmt)
+    x = special_matrix_f32(rng, 24, 512)
+    for scaling in ("pcs", "hw", "unit"):
+        for backoff in (1.0, 0.5, 2.0, 0.8):
+            q = O.quantize_with(x.ravel(), 24, 512, fmt, scaling, backoff)
+            codes, s, bias = quantize_f32_closed_form(x, fmt, scaling, backoff)
+            assert np.array_equal(q.scales.view(np.uint32), s.view(np.uint32)), (scaling, backoff)
+            assert q.exp_bias == bias, (scaling, backoff)
+            bad = np.nonzero(q.codes != codes)[0]
+            assert bad.size == 0, (scaling, backoff, bad[:5], q.codes[bad[:5]], codes[bad[:5]])
+    # The special cases land where the reference's arithmetic puts them.
+    q = O.quantize_with(x.ravel(), 24, 512, fmt, "pcs", 1.0)
+    c = q.codes.reshape(24, 512)
+    mx = MAXCODE[fmt]
+    assert q.scales[5] == 0.0 and q.scales[13] == 0.0          # 2^-149 / max and the 2^-150 tie underflow
+    if fmt == E4M3:
+        assert q.scales[14] == np.float32(2.0 ** -149)         # 121 * 2^-149 / 240 rounds up
+    assert 0 < q.scales[6] < np.finfo(np.float32).tiny and 0 < q.scales[7] < np.finfo(np.float32).tiny
+    row5 = x[5]
+    assert np.all(c[5][row5 == 0] == 0xFF)                     # 0 / 0: negative default NaN
+    assert np.all(c[5][row5 > 0] == mx) and np.all(c[5][row5 < 0] == (0x80 | mx))
+    assert np.isinf(q.scales[1]) and c[1, 5] == 0xFF           # inf / inf
+    assert np.all(c[1][np.isfinite(x[1]) & ~np.signbit(x[1])] == 0x00)
+    assert c[3, 11] == 0x7F and c[4, 0] == 0xFF                # NaN keeps its sign
+    assert q.scales[10] == 1.0 and np.all((c[10] & 0x7F) == 0x7F)
+    assert q.scales[8] == 1.0 and np.all(c[8] == 0) and np.all(c[9] == 0x80)
+    assert c[11, 0] == mx and c[11, 4] == 0x80 | mx
+
+
+def test_f32_quantize_a_planted_mistake_is_caught():
+    """The closed form rejects an oracle that multiplies by the reciprocal of s
+    instead of dividing (the slip an f32 fast path invites): on rows whose
+    quotients sit next to fp8 midpoints the two round apart."""
+    from helpers import quantize_f32_closed_form, positive_table
+
+    rng = np.random.default_rng(43)
+    _, vals = positive_table(E4M3)
+    mids = (vals[1:] + vals[:-1]) / 2
+    rows, cols = 64, 1024
+    m = np.exp(rng.uniform(np.log(1e-3), np.log(1e2), rows)).astype(np.float32)
+    s = (m / np.float32(240.0)).astype(np.float32)
+    x = np.empty((rows, cols), dtype=np.float32)
+    for r in range(rows):
+        base = (mids * np.float64(s[r])).astype(np.float32).view(np.int32)
+        cand = np.concatenate([base + d for d in (-1, 0, 1)]).view(np.float32)
+        cand = cand[np.abs(cand) <= m[r]]
+        x[r] = np.resize(rng.permutation(cand), cols)
+        x[r, 0] = m[r]
+    codes, s2, _ = quantize_f32_closed_form(x, E4M3, "pcs", 1.0)
+    assert np.array_equal(O.quantize_with(x.ravel(), rows, cols, E4M3, "pcs").codes, codes)
+    recip = nearest_encode((x * (np.float32(1.0) / s2)[:, None]).astype(np.float32), E4M3)
+    assert not np.array_equal(recip, codes)
