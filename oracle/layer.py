@@ -22,7 +22,11 @@ position 0 is the identity and every later position a rotation of each
 RMSNorm of a constant row in closed form; attention over one key returns its
 value and over equal scores the running mean of the values; zero output
 projections make the layer the identity; a later token never changes an
-earlier row (causality); GQA equals full attention over repeated k/v heads.
+earlier row (causality); GQA equals full attention over repeated k/v heads;
+the RoPE tables against transformers' own rows for the reference's unscaled
+case (tests/golden/rope_gemma3_local.json, from the reference's
+rope_reference.json); the SwiGLU branch against a float64 closed form on a
+hand-built layer whose gate and up differ (a swap would fail).
 """
 import numpy as np
 

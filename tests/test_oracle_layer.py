@@ -131,3 +131,67 @@ def test_the_attention_scale_multiplies_the_scores():
     assert np.allclose(a, b, rtol=1e-5, atol=1e-5)
     c = L.layer(x, w, nh, nkv, hd, 1e-5, sin, cos, 1.0)
     assert not np.allclose(a, c, rtol=1e-3)
+
+
+def test_rope_tables_match_the_transformers_reference():
+    """The reference's transformers-generated RoPE rows for its unscaled case
+    (tests/golden/rope_gemma3_local.json, copied from
+    crates/reng-model/testdata/rope_reference.json), with the tolerance of
+    rope_tables_match_the_transformers_reference (crates/reng-model/src/lib.rs:
+    3930-3960): 1e-6 plus the angle gap p * |inv_freq - inv_freq_ref|."""
+    import json
+    import os
+
+    fx = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "rope_gemma3_local.json")))
+    hd, theta = fx["head_dim"], fx["theta"]
+    assert fx["rotary_dim"] == hd and fx["attention_factor"] == 1.0
+    inv = L.rope_inv_freq(hd, theta)
+    ref_inv = np.asarray(fx["inv_freq"], dtype=F32)
+    assert inv.shape == ref_inv.shape
+    rel = np.abs(inv.astype(np.float64) - ref_inv) / np.abs(ref_inv.astype(np.float64))
+    assert rel.max() < 1e-6, rel.max()
+    sin, cos = L.rope_caches(fx["table_len"], hd, theta)
+    half = hd // 2
+    for row, p in enumerate(fx["positions"]):
+        j = np.arange(hd) % half
+        da = np.abs((F32(p) * inv[j]).astype(np.float64) - (F32(p) * ref_inv[j]).astype(np.float64))
+        tol = 1e-6 + da
+        assert np.all(np.abs(cos[p].astype(np.float64) - np.asarray(fx["cos"][row])) < tol), p
+        assert np.all(np.abs(sin[p].astype(np.float64) - np.asarray(fx["sin"][row])) < tol), p
+    # A plausible slip fails: tables indexed by d instead of d % half.
+    bad = np.sin((F32(fx["positions"][-1]) * L.rope_inv_freq(2 * hd, theta)[:hd]).astype(F32))
+    assert not np.all(np.abs(bad - np.asarray(fx["sin"][-1])) < 1e-3)
+
+
+def test_mlp_branch_closed_form():
+    """The SwiGLU branch y = x + wd (silu(n wg^T) * (n wu^T)) in float64 with
+    math.exp, on a hand-built layer: wo = 0 removes the attention branch, the
+    input row is constant so its RMSNorm is c / sqrt(c^2 + eps) * g2, and gate
+    and up are chosen unequal (so a swap, a missing silu or silu on the wrong
+    operand, or a transposed wd all give other numbers)."""
+    import math
+
+    hidden, inter, nh, nkv, hd, eps = 4, 3, 1, 1, 4, 1e-5
+    c = 0.5
+    x = np.full((1, hidden), c, dtype=F32)
+    g2 = np.array([1.0, 2.0, 0.5, 1.0], dtype=F32)
+    wg = np.array([[0.5, 0.25, 0.0, 0.0], [0.0, 0.0, -1.0, -1.0], [3.0, 0.0, 0.0, 0.0]], dtype=F32)
+    wu = np.array([[-1.0, 0.0, 0.0, 2.0], [0.5, 0.0, 0.0, 0.0], [0.0, 0.0, 0.0, -0.25]], dtype=F32)
+    wd = np.array([[1.0, 0.0, 0.5], [0.0, 1.0, 0.0], [2.0, -1.0, 0.0], [0.0, 0.5, -2.0]], dtype=F32)
+    rng = np.random.default_rng(11)
+    w = {"g1": np.ones(hidden, F32), "g2": g2,
+         "wq": rng.standard_normal((nh * hd, hidden)).astype(F32),
+         "wk": rng.standard_normal((nkv * hd, hidden)).astype(F32),
+         "wv": rng.standard_normal((nkv * hd, hidden)).astype(F32),
+         "wo": np.zeros((hidden, nh * hd), F32), "wg": wg, "wu": wu, "wd": wd}
+    sin, cos = L.rope_caches(1, hd, 10000.0)
+    got = L.layer(x, w, nh, nkv, hd, eps, sin, cos, hd ** -0.5)[0].astype(np.float64)
+    n = [c / math.sqrt(c * c + eps) * float(g) for g in g2]
+    gate = [sum(n[k] * float(wg[j, k]) for k in range(hidden)) for j in range(inter)]
+    up = [sum(n[k] * float(wu[j, k]) for k in range(hidden)) for j in range(inter)]
+    act = [g / (1.0 + math.exp(-g)) * u for g, u in zip(gate, up)]
+    want = [c + sum(float(wd[i, j]) * act[j] for j in range(inter)) for i in range(hidden)]
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6), (got, want)
+    swapped = [c + sum(float(wd[i, j]) * (u / (1.0 + math.exp(-u)) * g) for j, (g, u) in enumerate(zip(gate, up)))
+               for i in range(hidden)]
+    assert not np.allclose(swapped, want, rtol=1e-3)
