@@ -10,18 +10,21 @@ backoff 1. One step = one pass of the quantizer over the whole set, inputs
 already resident in HBM. Algorithmic bytes per element: 2 (bf16 in) + 1 (code
 out), plus 4 per row (f32 scale).
 
-Also reported (under "extras"): E5M2 over the same set; the f32 [2048, 2048]
-quantize rotated over 32 copies; the fused dequant GEMV at batch 1 on the
-[14336, 4096] and [4096, 14336] shapes rotated over 32 layers; the skinny GEMM at
-batch 8 and 64 on Qwen2.5-7B shapes; the M = 1024 fp8 x fp8 GEMM on
-Qwen2.5-32B shapes. With --extended, the full Qwen2.5-32B quantize.
+Also reported (under "extras"): E5M2 over the same set; the full Qwen2.5-32B-shaped
+quantize (64 layers, 31.2 G elements, layer 0 compared bit for bit with the
+oracle); the f32 [2048, 2048] quantize rotated over 32 copies (compared with the
+oracle); the fused dequant GEMV at batch 1 on the [14336, 4096] and
+[4096, 14336] shapes rotated past the Infinity Cache, next to a plain read of
+the same bytes (the one-launch read yardstick); the skinny GEMM at batch 8 and
+64 on Qwen2.5-7B shapes; the M = 1024 fp8 x fp8 GEMM on Qwen2.5-32B shapes; the
+fp8 decode step.
 
 The CPU baseline is the oracle (a C restatement of reng-fp8's quantizer: two
 passes, an IEEE divide per element, <= 8 threads by reng-fp8's split rule)
 timed on this host over layers 0-7 of the same set; those layers are also
 compared bit for bit with the GPU's codes and scales.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--extended]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--part ...]
 """
 import argparse
 import json
@@ -218,7 +221,7 @@ def rotation(nbytes, floor=4, cap=1024):
     return min(cap, n)
 
 
-def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3"):
+def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3", read_yardstick=False):
     per = N * K
     copies = rotation(per)
     ws = []
@@ -234,9 +237,18 @@ def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3"):
     nbytes = RC.w8a16_bytes(M, N, K)
     flops = 2 * M * N * K
     ceil = RC.w8a16_ceiling(MI355X, M, N, K)   # HBM-bound for M <= 64
-    return {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
-            "hbm_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value,
-            "TFLOPs": round(flops / secs / 1e12, 2), "rotated_copies": copies}
+    rec = {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
+           "hbm_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value,
+           "TFLOPs": round(flops / secs / 1e12, 2), "rotated_copies": copies}
+    if read_yardstick and (N * K) % 1024 == 0:
+        # A plain read of the same code bytes, rotated the same way: the
+        # fastest one launch of this size reads on this device.
+        sink = torch.empty(R.stream_read_sink_bytes(), dtype=torch.uint8, device="cuda")
+        rsecs = graph_time(torch, lambda i: R.stream_read(ws[i % copies][0], N * K, sink), max(2 * copies, 40))
+        rec["read_yardstick"] = {"us": round(rsecs * 1e6, 2), "GBps": round(N * K / rsecs / 1e9, 1),
+                                 "hbm_frac": round(N * K / rsecs / HBM_PEAK, 3),
+                                 "gemv_over_read": round(secs / rsecs, 3)}
+    return rec
 
 
 def bench_fp8_gemm(torch, R, gen, M, N, K):
@@ -283,11 +295,82 @@ def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048, cpu=False):
     rec = {"rows": rows, "cols": cols, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
            "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "rotated_copies": copies}
     if cpu:
+        import numpy as np
+
+        import oracle as O
+
+        torch.cuda.synchronize()
+        ref = O.quantize_with(mats[0][0].cpu().numpy(), rows, cols, "e4m3", "pcs", 1.0)
+        rec["parity"] = {"matrices": 1, "mismatched": int(not (
+            np.array_equal(mats[0][1].cpu().numpy(), ref.codes)
+            and np.array_equal(mats[0][2].cpu().numpy().view(np.uint32), ref.scales.view(np.uint32))))}
         us = cpu_f32_quantize(mats[0][0].cpu().numpy(), rows, cols)
         threads = max(1, min(8, (rows * cols) >> 20, rows))   # reng-fp8's split rule
         rec["cpu_baseline"] = {"us": round(us, 1), "GBps": round(nbytes / us / 1e3, 2), "threads": threads,
                                "kind": "port", "sample": "the first of the rotated matrices"}
     return rec
+
+
+def bench_qwen32b_quantize(torch, R, fmt="e4m3", steps=3, warmup=1, parity=True):
+    """The Qwen2.5-32B-shaped quantize: 64 layers of q/o [5120, 5120], k/v
+    [1024, 5120], gate/up [27648, 5120], down [5120, 27648] bf16, N(0, 0.02) with
+    the same injections, E4M3 per-channel; inputs resident in HBM. Layer 0's
+    seven matrices are compared bit for bit with the oracle."""
+    import numpy as np
+
+    t0 = time.perf_counter()
+    wq = WeightSet(torch, QWEN_32B, 64, seed=4321)
+    torch.cuda.synchronize()
+    gen_s = time.perf_counter() - t0
+    r = time_quantize(torch, R, wq, fmt, steps, warmup)
+    dom = r["dominant"]
+    rec = {"workload": "Qwen2.5-32B-shaped bf16 set, 64 layers x (q/o [5120,5120], k/v [1024,5120], "
+                       "gate/up [27648,5120], down [5120,27648]), N(0,0.02) with the same injections",
+           "format": fmt, "scaling": "pcs", "elements": wq.elements, "algorithmic_bytes_per_step": wq.bytes,
+           "steps": steps, "ms_per_step": round(r["step_s"] * 1e3, 3), "GBps": round(r["gbps"], 1),
+           "hbm_frac": round(r["gbps"] * 1e9 / HBM_PEAK, 4),
+           "per_row_width": {c: {"GBps": round(v["GBps"], 1), "hbm_frac": round(v["GBps"] * 1e9 / HBM_PEAK, 4),
+                                 "launches_per_step": v["launches_per_step"]} for c, v in r["configs"].items()},
+           "dominant": {"cols": dom["cols"], "mean_launch_us": round(dom["secs_per_launch"] * 1e6, 1),
+                        "algorithmic_bytes_per_launch": int(dom["bytes_per_launch"])},
+           "generated_in_s": round(gen_s, 1)}
+    if parity:
+        import oracle as O
+
+        bad = 0
+        for m in [m for m in wq.mats if m[0] == 0]:
+            ref = O.quantize_with(m[4].cpu().numpy().view(np.uint16), m[2], m[3], fmt, "pcs", 1.0)
+            bad += int(not (np.array_equal(m[5].cpu().numpy(), ref.codes)
+                            and np.array_equal(m[6].cpu().numpy().view(np.uint32), ref.scales.view(np.uint32))))
+        rec["parity"] = {"matrices": 7, "mismatched": bad, "sample": "layer 0 (q, k, v, o, gate, up, down)"}
+    del wq
+    torch.cuda.empty_cache()
+    return rec
+
+
+def bench_host_quantize(torch, R, layers=2, fmt="e4m3"):
+    """The host-pointer entry Rust's quantize_with calls (reng_hip_quantize_host:
+    pinned row chunks over two streams, upload, quantize and download
+    overlapped): Llama-3.1-8B layers 0..layers-1 from host memory, codes and
+    scales back in host memory. GB/s of the same algorithmic bytes, PCIe
+    included (never the headline value)."""
+    import numpy as np
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    mats = []
+    for _ in range(layers):
+        for name, rows, cols in LLAMA_8B:
+            mats.append((rows, cols, make_bf16(torch, rows, cols, gen).cpu().numpy().view(np.uint16)))
+    R.quantize_host(mats[0][2], mats[0][0], mats[0][1], fmt, "pcs")   # staging buffers, first touch
+    t0 = time.perf_counter()
+    for rows, cols, w in mats:
+        R.quantize_host(w, rows, cols, fmt, "pcs")
+    secs = time.perf_counter() - t0
+    nbytes = sum(quant_bytes(r, c) for r, c, _ in mats)
+    return {"matrices": len(mats), "algorithmic_bytes": nbytes, "secs": round(secs, 4),
+            "GBps": round(nbytes / secs / 1e9, 2), "layers": layers, "format": fmt,
+            "note": "host memory in and out, PCIe and host copies included"}
 
 
 def bench_decode_step(layers=4, positions=512):
@@ -385,9 +468,8 @@ def main():
     ap.add_argument("--format", default="e4m3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--extended", action="store_true", help="also the full Qwen2.5-32B quantize")
     ap.add_argument("--part", default="all",
-                    choices=["all", "quantize", "gemv", "skinny", "prefill", "f32", "decode"],
+                    choices=["all", "quantize", "gemv", "skinny", "prefill", "f32", "decode", "qwen32b", "host"],
                     help="run one part only (for profiling); the JSON line is printed for 'all' and 'quantize'")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy 1 GiB device-to-device three times first: a kernel of known traffic that "
@@ -418,7 +500,12 @@ def main():
         gen = torch.Generator(device="cuda")
         gen.manual_seed(99)
         if args.part == "gemv":
-            out = [bench_w8a16(torch, R, gen, 1, 14336, 4096), bench_w8a16(torch, R, gen, 1, 4096, 14336)]
+            out = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
+                   bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True)]
+        elif args.part == "qwen32b":
+            out = [bench_qwen32b_quantize(torch, R, args.format, parity=not args.no_cpu)]
+        elif args.part == "host":
+            out = [bench_host_quantize(torch, R)]
         elif args.part == "skinny":
             out = [bench_w8a16(torch, R, gen, M, N, K) for M in (8, 64) for _, N, K in QWEN_7B]
         elif args.part == "prefill":
@@ -468,9 +555,13 @@ def main():
         torch.cuda.empty_cache()
         gen = torch.Generator(device="cuda")
         gen.manual_seed(99)
+        extras["quantize_qwen32b"] = bench_qwen32b_quantize(torch, R, args.format, parity=not args.no_cpu)
+        log("qwen32b quantize:", extras["quantize_qwen32b"])
+        extras["quantize_host_llama8b"] = bench_host_quantize(torch, R)
+        log("host-pointer quantize:", extras["quantize_host_llama8b"])
         extras["f32_2048x2048_quantize"] = bench_f32_quantize(torch, R, gen, cpu=not args.no_cpu)
-        extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096),
-                                     bench_w8a16(torch, R, gen, 1, 4096, 14336)]
+        extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
+                                     bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True)]
         log("gemv b1:", extras["gemv_b1_llama8b"])
         sk = []
         for M in (8, 64):
@@ -488,12 +579,6 @@ def main():
         if not args.no_cpu and "error" not in extras["decode_step_llama8b"]:
             extras["decode_step_llama8b"]["cpu_baseline"] = decode_cpu_record()
         log("decode step:", extras["decode_step_llama8b"])
-        if args.extended:
-            wq = WeightSet(torch, QWEN_32B, 64, seed=4321)
-            r3 = time_quantize(torch, R, wq, "e4m3", 3, 1)
-            extras["quantize_qwen32b_e4m3"] = {"elements": wq.elements, "ms_per_step": round(r3["step_s"] * 1e3, 2),
-                                               "GBps": round(r3["gbps"], 1)}
-            del wq
 
     out = {
         "metric": METRIC,

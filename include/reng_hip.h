@@ -301,6 +301,15 @@ RENG_HIP_API int reng_hip_add_bf16_f32(const float *x, const uint16_t *d, size_t
 RENG_HIP_API int reng_hip_verify_hw_convert(int format, uint64_t *mismatches,
                                             uint32_t *first_mismatch);
 
+/* The read yardstick the GEMV is measured against: reads `bytes` (a positive
+ * multiple of 1024, p 16-byte aligned) once, as 1 KB chunks dealt to 32 waves
+ * per CU in turn, one chunk per wave in flight (the fastest pattern found for
+ * a single read-only launch of GEMV size on MI355X). Computes nothing; sink is
+ * device memory of reng_hip_stream_read_sink_bytes() bytes that the kernel
+ * writes only if the data's XOR hits a fixed value. Asynchronous. */
+RENG_HIP_API size_t reng_hip_stream_read_sink_bytes(void);
+RENG_HIP_API int reng_hip_stream_read(const void *p, size_t bytes, void *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,8 +31,13 @@ int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *sca
 int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st);
 // A grow-only f32 workspace of at least `floats` for split-K partials, one per
-// (device, stream) (csrc/gemm.hip); sets *rc.
+// (device, stream) (csrc/gemm.hip); sets *rc. It refuses to grow while the
+// stream is being captured into a graph.
 float *split_workspace(size_t floats, hipStream_t st, int *rc);
+// The read yardstick: bytes / 1024 whole 1 KB chunks of p read once; sink
+// holds stream_read_sink_words() words (written only by chance).
+int launch_stream_read(const void *p, size_t bytes, uint32_t *sink, hipStream_t st);
+uint32_t stream_read_sink_words();
 int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, const uint8_t *b,
                     int fb, const float *sb, uint32_t nsb, uint32_t M, uint32_t N, uint32_t K,
                     uint16_t *out, hipStream_t st);

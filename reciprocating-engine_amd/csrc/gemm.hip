@@ -298,13 +298,239 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
     }
 }
 
-// ------------------------------------------------------------------ skinny GEMM
+// ------------------------------------------------------------------ GEMV, M = 1
+
+// One wave streams R consecutive rows of the codes (R K contiguous bytes) in
+// steps of U 1 KB chunks, the next step requested before the current one is
+// consumed, every wave resident from the start. Measured on MI355X against the
+// row-strided walk of gemv_w8a16 (whose waves read one row here, one row
+// 14 MB away there): [14336, 4096] 10.95 -> 10.2-10.5 us, [4096, 14336]
+// 11.6 -> 10.3 us, with a plain 1 KB-chunk read of the same bytes at 9.6-9.8 us.
+//
+// The activation is copied into LDS by global_load_lds before the first codes
+// are requested, and the wave waits only for those copies (vmcnt(U): the U
+// code loads issued after them may still be in flight) before the barrier.
+//
+// A lane takes the same 16 codes of every 1 KB chunk (k = 1024 c + 16 lane ..
+// + 16) and adds the products in gemv_w8a16's order (chunks in order, even and
+// odd words into two accumulators, then wave_sum_dpp), so the two kernels give
+// the same bits and the fused forms of gemv_w8a16 equal this GEMV followed by
+// their epilogue. A ragged last chunk (K % 1024 != 0) masks the lanes past K.
+__device__ __forceinline__ void dma16(const void *g, void *l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void gemv_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | (7 << 4) | (0xf << 8) | ((N >> 4) << 14));
+}
+
+// Loads the compiler does not track: it inserts no wait for them (and so
+// none that would also wait for the next step's loads); the kernel waits with
+// gemv_wait_vmcnt and ties each result to that wait with gemv_after_wait. The
+// codes are addressed as a wave-uniform base (SGPRs) plus a 32-bit lane offset.
+__device__ __forceinline__ u32x4 gemv_load16(const uint8_t *base, uint32_t off) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(v) : "v"(off), "s"(base) : "memory");
+    return v;
+}
+__device__ __forceinline__ float gemv_load4(const void *p) {
+    float v;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+template <int U>
+__device__ __forceinline__ void gemv_after_wait(u32x4 (&q)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) asm volatile("" : "+v"(q[u]));
+}
+// s_waitcnt vmcnt(n) for a run-time n <= 7.
+__device__ __forceinline__ void gemv_wait_upto(uint32_t n) {
+    switch (n) {
+        case 0: gemv_wait_vmcnt<0>(); break;
+        case 1: gemv_wait_vmcnt<1>(); break;
+        case 2: gemv_wait_vmcnt<2>(); break;
+        case 3: gemv_wait_vmcnt<3>(); break;
+        case 4: gemv_wait_vmcnt<4>(); break;
+        case 5: gemv_wait_vmcnt<5>(); break;
+        case 6: gemv_wait_vmcnt<6>(); break;
+        default: gemv_wait_vmcnt<7>(); break;
+    }
+}
+
+template <int F, int U, int WPB, bool RAG>
+__global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *__restrict__ x,
+                                                      const uint8_t *__restrict__ codes,
+                                                      const float *__restrict__ scales, uint32_t N, uint32_t K,
+                                                      uint32_t R, uint16_t *__restrict__ y) {
+    static_assert(U >= 1 && U <= 7, "gemv_wait_upto covers up to 7 loads in flight");
+    extern __shared__ __attribute__((aligned(16))) uint32_t xs_words[];
+    uint8_t *xs = reinterpret_cast<uint8_t *>(xs_words);   // the activation, K bf16
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t cpr = (K + 1023) >> 10;            // 1 KB chunks per row
+    const uint32_t spr = (cpr + U - 1) / U;           // steps per row (the last may be short)
+    const uint32_t live = (K & 1023) ? (K & 1023) >> 4 : 64;   // lanes of the last chunk inside the row
+    const uint32_t r0 = w * R;
+    const uint32_t rows = r0 < N ? (N - r0 < R ? N - r0 : R) : 0;
+    const uint8_t *wbase = codes + (size_t)(r0 < N ? r0 : 0) * K;   // this wave's rows, R K contiguous bytes
+
+    // In issue order (the waits count on it): this lane's row scale (lane j
+    // holds row r0 + j, R <= 64), the activation copies, the first step.
+    const float sraw = gemv_load4(scales && rows ? static_cast<const void *>(scales + r0 + ((uint32_t)lane < rows ? lane : 0))
+                                                 : static_cast<const void *>(codes));
+    // Activation: piece i (8 bf16, 16 bytes) by thread i mod 64 WPB.
+    for (uint32_t i = tid; i < K / 8; i += 64 * WPB) dma16(x + 8 * (size_t)i, xs + 16 * (size_t)(i - lane));
+
+    // Step j of row r: chunks [j U, min((j + 1) U, cpr)) of the row; steps never
+    // span two rows, so a row ends with its last step.
+    auto step_loads = [&](uint32_t r, uint32_t j) -> uint32_t {   // chunks the step holds (0: none)
+        if (r >= rows) return 0;
+        const uint32_t left = cpr - j * U;
+        return left < U ? left : U;
+    };
+    auto issue = [&](u32x4 (&q)[U], uint32_t r, uint32_t j) {
+        const uint32_t n = step_loads(r, j);
+        const uint32_t base = r * K + j * U * 1024;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if ((uint32_t)u < n) {
+                const bool lastc = RAG && j * U + u + 1 == cpr;
+                const uint32_t lanec = lastc && (uint32_t)lane >= live ? live - 1 : lane;
+                q[u] = gemv_load16(wbase, base + u * 1024 + 16 * lanec);
+            }
+        }
+    };
+
+    uint32_t r = 0, j = 0;                            // the step being consumed
+    float a0 = 0.0f, a1 = 0.0f;
+    float sv = 1.0f;
+    // One step: n chunks (n == U: no guard), then the row's end when j is its
+    // last step.
+    auto consume = [&](const u32x4 (&q)[U], uint32_t n) {
+        const uint8_t *xrow = xs + 2 * ((size_t)j * U * 1024 + 16 * lane);
+        auto chunk = [&](int u) {
+            uint32_t wv[8];
+            decode16<F>(q[u], wv);
+            const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow + u * 2048);
+            u32x4 xa, xb;
+            if (RAG && j * U + u + 1 == cpr && (uint32_t)lane >= live) {
+                // Past K in a ragged last chunk: no codes, and no activation
+                // past the LDS copy either.
+#pragma unroll
+                for (int i = 0; i < 8; ++i) wv[i] = 0u;
+                xa = xb = u32x4{0u, 0u, 0u, 0u};
+            } else {
+                xa = xp[0];
+                xb = xp[1];
+            }
+            a0 = dot2(wv[0], xa.x, a0);
+            a1 = dot2(wv[1], xa.y, a1);
+            a0 = dot2(wv[2], xa.z, a0);
+            a1 = dot2(wv[3], xa.w, a1);
+            a0 = dot2(wv[4], xb.x, a0);
+            a1 = dot2(wv[5], xb.y, a1);
+            a0 = dot2(wv[6], xb.z, a0);
+            a1 = dot2(wv[7], xb.w, a1);
+        };
+        if (n == U) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) chunk(u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if ((uint32_t)u < n) chunk(u);
+        }
+        if (j + 1 == spr) {   // the row's last step
+            const float t = wave_sum_dpp(a0 + a1);
+            const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), r));
+            if (lane == 0) y[r0 + r] = (uint16_t)f32_to_bf16_bits(t * s);
+            a0 = a1 = 0.0f;
+            j = 0;
+            ++r;
+        } else {
+            ++j;
+        }
+    };
+    auto next_of = [&](uint32_t rr, uint32_t jj, uint32_t &rn, uint32_t &jn) {
+        if (jj + 1 == spr) {
+            rn = rr + 1;
+            jn = 0;
+        } else {
+            rn = rr;
+            jn = jj + 1;
+        }
+    };
+
+    // Two register sets, used in turn: step s + 1 is requested before step s
+    // is waited for and consumed (requesting two steps ahead, or a wave's
+    // whole rows at once, measured slower: more of the matrix in flight at
+    // the start of the launch); nothing is requested past the wave's rows.
+    u32x4 qa[U], qb[U];
+    issue(qa, 0, 0);
+    gemv_wait_upto(step_loads(0, 0));   // the scale and the activation copies have landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    sv = scales ? sraw : 1.0f;
+    while (r < rows) {
+        uint32_t rn, jn;
+        next_of(r, j, rn, jn);
+        const uint32_t na = step_loads(r, j), nb = step_loads(rn, jn);
+        issue(qb, rn, jn);
+        gemv_wait_upto(nb);   // qa's step has landed; qb's may still be in flight
+        gemv_after_wait(qa);
+        consume(qa, na);
+        if (r >= rows) break;
+        next_of(r, j, rn, jn);
+        const uint32_t nb2 = step_loads(r, j), na2 = step_loads(rn, jn);
+        issue(qa, rn, jn);
+        gemv_wait_upto(na2);
+        gemv_after_wait(qb);
+        consume(qb, nb2);
+    }
+}
+
+// ------------------------------------------------------------------ read yardstick
+
+// Reads `chunks` 1 KB chunks: wave w takes chunks w, w + W, ... one at a time
+// (16-byte non-temporal loads, one 1 KB chunk per wave in flight), the pattern
+// that read a GEMV-sized buffer fastest on this device (measured over 1-8
+// chunks in flight per wave and 8-32 waves per CU). The XOR of the data keeps
+// the loads live; sink is written only if the XOR hits a fixed value, so the
+// launch writes (almost) nothing.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4 *__restrict__ p, uint64_t chunks,
+                                                          uint32_t *sink) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t W = (uint64_t)gridDim.x * 4, w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    uint32_t acc = 0;
+    for (uint64_t c = w; c < chunks; c += W) {
+        const u32x4 v = __builtin_nontemporal_load(p + c * 64 + lane);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+int launch_stream_read(const void *p, size_t bytes, uint32_t *sink, hipStream_t st) {
+    const uint32_t blocks = (uint32_t)device_props().cus * 8;   // 32 waves per CU
+    hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, st, static_cast<const u32x4 *>(p),
+                       (uint64_t)(bytes / 1024), sink);
+    return check_launch("stream_read");
+}
+
+uint32_t stream_read_sink_words() { return (uint32_t)device_props().cus * 8; }
 
 // ------------------------------------------------------------------ launchers
 
 // Split-K partials live in a grow-only f32 buffer per (device, stream): calls on
 // one stream are ordered, so they can share it; calls on different streams get
 // different buffers. No allocation once a stream has seen its largest product.
+// The buffers live until the process ends (keyed by the stream handle: a
+// stream destroyed while its work is still queued must not have its handle
+// reused by another before that work ends). Growing it synchronizes the stream
+// and calls hipMalloc, which a stream under graph capture cannot do: that case
+// is refused (warm the stream up with the largest product first).
 float *split_workspace(size_t floats, hipStream_t st, int *rc) {
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, std::pair<float *, size_t>> bufs;
@@ -313,6 +539,14 @@ float *split_workspace(size_t floats, hipStream_t st, int *rc) {
     std::lock_guard<std::mutex> lk(mu);
     auto &e = bufs[{dev, st}];
     if (e.second < floats) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+            set_error("the split-K workspace would grow to %zu bytes while the stream is captured: run the "
+                      "product once on this stream before capturing",
+                      floats * sizeof(float));
+            *rc = RENG_HIP_EINVAL;
+            return nullptr;
+        }
         if (e.first) {
             // The old buffer may still be read by work queued on this stream.
             const hipError_t se = hipStreamSynchronize(st);
@@ -461,9 +695,45 @@ int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *sca
                                                               0.0f, st);
 }
 
+// gemv_rows's launch: about 28 waves per CU (one round: every wave resident)
+// with R = ceil(N / waves) consecutive rows each, at most 64; 7-chunk steps
+// when rows split into whole groups of 7 KB (K = 14336), else 4; 8-wave
+// workgroups for rows of 8 KB or more (one activation copy per 8 waves), else 4.
+template <int F>
+int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                     uint16_t *y, hipStream_t st) {
+    const uint32_t cpr = (K + 1023) / 1024;
+    const bool rag = (K & 1023) != 0;
+    // Waves per CU that stay resident: 8 per SIMD for the 4-chunk form
+    // (61 VGPRs), 5 for the 7-chunk and ragged forms (87-89 VGPRs).
+    const uint32_t per_cu = (cpr % 7 != 0 && !rag) ? 28 : 20;
+    const uint32_t target = (uint32_t)device_props().cus * per_cu;
+    uint32_t R = (N + target - 1) / target;
+    R = R < 1 ? 1 : R > 64 ? 64 : R;
+    const uint32_t waves = (N + R - 1) / R;
+    const size_t lds = (size_t)K * 2;
+#define RENG_ROWS(UU, WW, RG)                                                                                    \
+    hipLaunchKernelGGL((gemv_rows<F, UU, WW, RG>), dim3((waves + WW - 1) / WW), dim3(64 * WW), lds, st, x, codes, \
+                       scales, N, K, R, y)
+    if (cpr % 7 == 0 && !rag) RENG_ROWS(7, 8, false);
+    else if (cpr >= 8) {
+        if (rag) RENG_ROWS(4, 8, true);
+        else RENG_ROWS(4, 8, false);
+    } else {
+        if (rag) RENG_ROWS(4, 4, true);
+        else RENG_ROWS(4, 4, false);
+    }
+#undef RENG_ROWS
+    return check_launch("gemv_rows");
+}
+
 template <int F>
 int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
+    // One activation row: the contiguous-rows GEMV while the row fits in LDS
+    // (64 KB); x and codes are 16-byte aligned (checked by the entry point).
+    if (M == 1 && K <= 32768)
+        return launch_gemv_rows<F>(x, codes, scales, N, K, y, st);
     if (M > 4 && K % 128 != 0) {
         // The MFMA kernel walks K in 128-code chunks; other widths take the
         // GEMV kernel four activation rows at a time.

@@ -6,8 +6,8 @@
 // workgroup owns a row at a time, holds it in registers between the two
 // phases and so reads HBM once: rows*cols*(in_bytes + 1) + 4*rows bytes.
 //
-// Fast path (a row with no NaN and a finite non-zero scale s, subnormal s
-// included): q = RN32(x * RN64(1/s)) computed in f64 IS the IEEE f32 quotient
+// Fast path (a row with no NaN and a finite normal scale s): q = RN32(x * RN64(1/s))
+// computed in f64 IS the IEEE f32 quotient
 // RN32(x / s) that the reference encodes, for every finite x:
 //   * x * RN64(1/s) is within |z| * 2^-52 of z = x / s (two f64 roundings);
 //   * the quotient of two 24-bit floats is never an f32 midpoint, and when it
@@ -20,9 +20,13 @@
 // every input of magnitude below the first out-of-range midpoint (248 /
 // 61440): checked on all 2^32 patterns by reng_hip_verify_hw_convert. Inputs
 // that could reach that range (HW and UNIT scales, or a backoff above 1) are
-// clamped first with v_med3 (saturation is monotone).
-// Slow rows (a NaN present, s = inf or 0) use the IEEE divide and the exact
-// integer encoder for every element, with x86's NaN semantics.
+// clamped first with v_med3 (saturation is monotone). A per-channel scale
+// s = RN32(m / (max * backoff)) that is normal is within 2^-24 of the exact
+// ratio, so with backoff <= 1 no |x / s| passes max * (1 + 2^-23) and no clamp
+// is needed; a subnormal s carries fewer significant bits (s = 4 * 2^-149 for
+// m = 1000 * 2^-149, E4M3: x / s = 250), so those rows take the slow path.
+// Slow rows (a NaN present, s = inf, 0 or subnormal) use the IEEE divide and
+// the exact integer encoder for every element, with x86's NaN semantics.
 #include "common.h"
 #include "quantize.h"
 
@@ -193,9 +197,11 @@ __global__ __launch_bounds__(64 * WAVES) void quantize_rows_fast(QBatch B, int s
         // Phase 2: codes from registers. q = RN32(x * RN64(1/s)) equals the
         // IEEE f32 quotient RN32(x / s) for every finite x and every finite
         // non-zero s (see the top of this file), so each code is one f64
-        // multiply and one hardware conversion.
+        // multiply and one hardware conversion; rows whose s is subnormal
+        // (fewer significant bits: |x / s| may pass the clamp-free range) or
+        // not finite and positive take the exact path.
         uint32_t c[VPT][CPV];
-        const bool fast = !has_nan && s > 0.0f && s < __builtin_inff();
+        const bool fast = !has_nan && s >= 1.17549435e-38f && s < __builtin_inff();
         if (fast) {
             const double R = 1.0 / (double)s;
 #pragma unroll
@@ -492,8 +498,9 @@ int launch_quantize_group(const QBatch &b, int dtype, int format, int scheme, fl
         fb = bias;
     }
     // The conversions are only exact up to the format's largest finite value;
-    // per-channel scales with backoff <= 1 keep |x / s| <= max_finite * (1 + 2^-22),
-    // which rounds to the largest code without a clamp.
+    // per-channel scales with backoff <= 1 keep |x / s| <= max_finite * (1 + 2^-23)
+    // for a normal s, which rounds to the largest code without a clamp (the
+    // kernel sends rows with a subnormal s to its exact path).
     const bool clamp = !(scheme == RENG_HIP_PCS && backoff <= 1.0f);
     int rc;
     if (dtype == RENG_HIP_BF16) {

@@ -282,10 +282,13 @@ Fp8Report LlamaWeights::quantize_fp8(const LlamaConfig &cfg, const Fp8Config &q)
     double err_sum = 0.0;
     size_t err_n = 0;
     float err_max = 0.0f;
-    // One device staging area for the whole pass: the bf16 matrix goes up
-    // once, the quantizer and the sampled error pass read it there, and the
-    // codes and scales come back.
-    DeviceBuf dw, dc, ds, deb, dmean, dmax;
+    // Each matrix goes through reng_hip_quantize_host (the library's pinned,
+    // double-buffered staging: upload, quantize and download of neighbouring
+    // row chunks overlap). The error sample needs only its eight rows on the
+    // device: they are gathered with their codes and scales and measured as
+    // an 8-row matrix (rows are independent, so the statistics are the
+    // sampled rows' own).
+    DeviceBuf dw, dc, ds, dmean, dmax;
     std::vector<LayerFp8> out;
     out.reserve(layers.size());
     for (size_t li = 0; li < layers.size(); ++li) {
@@ -299,23 +302,6 @@ Fp8Report LlamaWeights::quantize_fp8(const LlamaConfig &cfg, const Fp8Config &q)
                 throw std::invalid_argument("empty shape " + std::to_string(rows) + " x " + std::to_string(cols));
             if (!(q.backoff > 0.0f && std::isfinite(q.backoff)))
                 throw std::invalid_argument("backoff " + f32_shortest(q.backoff) + " is not positive and finite");
-            dw.reserve(w.size() * 2);
-            dc.reserve(w.size());
-            ds.reserve(rows * 4);
-            deb.reserve(4);
-            dmean.reserve(FP8_ERROR_ROWS * 4);
-            dmax.reserve(FP8_ERROR_ROWS * 4);
-            check_hip(hipMemcpy(dw.p, w.data(), w.size() * 2, hipMemcpyHostToDevice), "hipMemcpy H2D");
-            check_abi(reng_hip_quantize(dw.p, RENG_HIP_BF16, rows, cols, cols, (int)q.format, (int)q.scaling,
-                                        q.backoff, static_cast<uint8_t *>(dc.p), static_cast<float *>(ds.p),
-                                        static_cast<uint32_t *>(deb.p), nullptr));
-            // sample_row_errors(w, q, FP8_ERROR_ROWS): every ceil(rows / n)-th row.
-            const size_t n = std::min(FP8_ERROR_ROWS, rows);
-            const size_t step = (rows + n - 1) / n, k = (rows + step - 1) / step;
-            check_abi(reng_hip_row_errors(static_cast<const uint16_t *>(dw.p), static_cast<const uint8_t *>(dc.p),
-                                          static_cast<const float *>(ds.p), rows, cols, (int)q.format,
-                                          FP8_ERROR_ROWS, static_cast<float *>(dmean.p),
-                                          static_cast<float *>(dmax.p), nullptr));
             reng_fp8::Quantized r;
             r.format = q.format;
             r.scaling = q.scaling;
@@ -323,10 +309,32 @@ Fp8Report LlamaWeights::quantize_fp8(const LlamaConfig &cfg, const Fp8Config &q)
             r.cols = cols;
             r.codes.resize(rows * cols);
             r.scales.resize(rows);
+            check_abi(reng_hip_quantize_host(w.data(), RENG_HIP_BF16, rows, cols, (int)q.format, (int)q.scaling,
+                                             q.backoff, r.codes.data(), r.scales.data(), &r.exp_bias));
+            // sample_row_errors(w, q, FP8_ERROR_ROWS): every ceil(rows / n)-th row.
+            const size_t n = std::min(FP8_ERROR_ROWS, rows);
+            const size_t step = (rows + n - 1) / n, k = (rows + step - 1) / step;
+            std::vector<uint16_t> sw(k * cols);
+            std::vector<uint8_t> sc(k * cols);
+            std::vector<float> ss(k);
+            for (size_t j = 0; j < k; ++j) {
+                const size_t row = j * step;
+                std::memcpy(&sw[j * cols], w.data() + row * cols, cols * 2);
+                std::memcpy(&sc[j * cols], &r.codes[row * cols], cols);
+                ss[j] = r.scales[row];
+            }
+            dw.reserve(k * cols * 2);
+            dc.reserve(k * cols);
+            ds.reserve(k * 4);
+            dmean.reserve(k * 4);
+            dmax.reserve(k * 4);
+            check_hip(hipMemcpy(dw.p, sw.data(), k * cols * 2, hipMemcpyHostToDevice), "hipMemcpy H2D");
+            check_hip(hipMemcpy(dc.p, sc.data(), k * cols, hipMemcpyHostToDevice), "hipMemcpy H2D");
+            check_hip(hipMemcpy(ds.p, ss.data(), k * 4, hipMemcpyHostToDevice), "hipMemcpy H2D");
+            check_abi(reng_hip_row_errors(static_cast<const uint16_t *>(dw.p), static_cast<const uint8_t *>(dc.p),
+                                          static_cast<const float *>(ds.p), k, cols, (int)q.format, 0,
+                                          static_cast<float *>(dmean.p), static_cast<float *>(dmax.p), nullptr));
             std::vector<float> mean(k), mx(k);
-            check_hip(hipMemcpy(r.codes.data(), dc.p, rows * cols, hipMemcpyDeviceToHost), "hipMemcpy D2H");
-            check_hip(hipMemcpy(r.scales.data(), ds.p, rows * 4, hipMemcpyDeviceToHost), "hipMemcpy D2H");
-            check_hip(hipMemcpy(&r.exp_bias, deb.p, 4, hipMemcpyDeviceToHost), "hipMemcpy D2H");
             check_hip(hipMemcpy(mean.data(), dmean.p, k * 4, hipMemcpyDeviceToHost), "hipMemcpy D2H");
             check_hip(hipMemcpy(mx.data(), dmax.p, k * 4, hipMemcpyDeviceToHost), "hipMemcpy D2H");
             report.matrices += 1;

@@ -73,6 +73,8 @@ SIGNATURES = {
     "reng_hip_attention_decode_split": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P, _SZ, _P, _P]),
     "reng_hip_silu_mul_bf16": (_I, [_P, _P, _SZ, _P, _P]),
     "reng_hip_add_bf16_f32": (_I, [_P, _P, _SZ, _P, _P]),
+    "reng_hip_stream_read_sink_bytes": (_SZ, []),
+    "reng_hip_stream_read": (_I, [_P, _SZ, _P, _P]),
 }
 
 
@@ -520,6 +522,17 @@ def add_bf16_f32(x, d, n, out=None):
     _check(lib().reng_hip_add_bf16_f32(_dev(x, "x", 4 * n), _dev(d, "d", 2 * n), n, _dev(out, "out", 4 * n),
                                        _stream()))
     return out
+
+
+def stream_read(buf, nbytes, sink):
+    """The read yardstick: read nbytes of buf once (a device tensor; sink a
+    device tensor of at least stream_read_sink_bytes() bytes)."""
+    _check(lib().reng_hip_stream_read(_dev(buf, "buf", nbytes), nbytes,
+                                      _dev(sink, "sink", lib().reng_hip_stream_read_sink_bytes()), _stream()))
+
+
+def stream_read_sink_bytes():
+    return int(lib().reng_hip_stream_read_sink_bytes())
 
 
 def verify_hw_convert(fmt):

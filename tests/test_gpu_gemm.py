@@ -21,6 +21,32 @@ torch = pytest.importorskip("torch")
 TOL = 1e-2
 
 
+def assert_elementwise(got, a, b, K, what, acc=None):
+    """Every output against float64 numpy (an independent product): with
+    want = a b^T and s = |a| |b|^T in float64,
+        |got - want| <= 2^-8 |want| + acc s,
+    the bf16 rounding of the output plus the accumulation error, by default
+    acc = 1.01 (K / 64 + 16) 2^-23: IEEE f32 additions, at most K / 32 + 32 in
+    sequence (the VALU dot products and the bf16 MFMA). The fp8 MFMA adds each
+    instruction's 64 products at a lower internal precision (measured: about
+    2^-18 s at K = 384), so its callers pass acc = 2^-15. A wrong scale on one
+    output row, a dropped or repeated chunk, or a swapped tile edge breaks the
+    bound on the outputs it touches, where an aggregate rel-L2 would not."""
+    a = np.asarray(a, dtype=np.float64).reshape(-1, K)
+    b = np.asarray(b, dtype=np.float64).reshape(-1, K)
+    want = a @ b.T
+    s = np.abs(a) @ np.abs(b).T
+    got = np.asarray(got, dtype=np.float64).reshape(want.shape)
+    if acc is None:
+        acc = 1.01 * (K / 64 + 16) * 2.0 ** -23
+    bound = 2.0 ** -8 * np.abs(want) + acc * s
+    bad = np.abs(got - want) > bound
+    if bad.any():
+        i, j = np.argwhere(bad)[0]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outputs outside the bound; first [{i}, {j}]: "
+                             f"got {got[i, j]!r} want {want[i, j]!r} bound {bound[i, j]!r}")
+
+
 @pytest.fixture(scope="module")
 def R():
     import reng_hip
@@ -62,6 +88,8 @@ def check_w8a16(R, rng, M, N, K, fmt, sample_cols=None):
     rel = O.rel_l2(got.ravel(), want.ravel())
     assert rel < TOL, f"M={M} N={N} K={K} fmt={fmt}: rel_L2 {rel}"
     assert np.all(np.isfinite(y))
+    rows = slice(None) if sample_cols is None else idx
+    assert_elementwise(got, bf16_f32(x), deq.reshape(N, K)[rows], K, f"M={M} N={N} K={K} fmt={fmt}")
     return rel
 
 
@@ -97,6 +125,31 @@ def test_gemv_batch1_llama_8b_shapes(R, fmt, shape):
     rng = np.random.default_rng(101 + fmt)
     N, K = shape
     check_w8a16(R, rng, 1, N, K, fmt)
+
+
+@pytest.mark.parametrize("N,K", [(1, 16), (7, 1040), (1000, 3584), (7169, 18944), (300, 32768), (64, 33792),
+                                 (20000, 512), (129, 14336)])
+def test_gemv_batch1_contiguous_rows(R, N, K):
+    """M = 1 on the contiguous-rows GEMV: ragged last chunks (K % 1024 != 0),
+    fewer rows than waves, a row count that leaves the last wave short, the
+    64 KB activation limit and one past it (the row-strided GEMV then), both
+    formats, with and without the scale operand."""
+    rng = np.random.default_rng(N + K)
+    check_w8a16(R, rng, 1, N, K, E4M3 if N % 2 else E5M2)
+    q = quantized_weight(rng, N, K, E4M3)
+    x = bf16_bits(rng.standard_normal(K).astype(np.float32))
+    y = bf16_out(R.gemm_w8a16(dev(x), dev(q.codes), None, 1, N, K, E4M3))
+    assert_elementwise(y.reshape(1, N), bf16_f32(x), O.decode_array(q.codes, E4M3).reshape(N, K), K, "unit scale")
+
+
+def test_gemv_refuses_an_unaligned_activation(R):
+    """The activation and the codes are read in 16-byte pieces: a pointer off
+    that alignment is refused before any launch."""
+    K = 4096
+    x = torch.zeros(K + 8, dtype=torch.int16, device="cuda")
+    c = torch.zeros(8 * K, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        R.gemm_w8a16(x[1:K + 1], c, None, 1, 8, K, E4M3)
 
 
 @pytest.mark.parametrize("M", [2, 3, 4])
@@ -164,6 +217,14 @@ def test_skinny_wide_block_shapes(R, M, N, K):
     check_w8a16(R, rng, M, N, K, fmt, sample_cols=None if N * K <= 4096 * 384 else 512)
 
 
+@pytest.mark.parametrize("M", [8, 64])
+def test_skinny_every_output_of_a_qwen_7b_gate_up(R, M):
+    """Every output of the Qwen2.5-7B gate/up product [18944, 3584] at M = 8 and
+    64, each element against float64 numpy within the bound above."""
+    rng = np.random.default_rng(401 + M)
+    check_w8a16(R, rng, M, 18944, 3584, E4M3)
+
+
 def test_the_reference_probe_shapes(R):
     """fp8_probe.rs:478-505: weights(512, 256), m in {1, 256}, rel_L2 < 0.02."""
     N, K = 512, 256
@@ -217,6 +278,9 @@ def check_fp8(R, rng, M, N, K, fa, fb, act="pcs", nsb="N", sample_cols=None):
         got = out
     rel = O.rel_l2(got.ravel(), want.ravel())
     assert rel < TOL, f"M={M} N={N} K={K} {fa}x{fb} act={act} sb={nsb}: rel_L2 {rel}"
+    rows = idx if sample_cols and sample_cols < N else slice(None)
+    assert_elementwise(got, a_deq, b_deq.reshape(N, K)[rows], K, f"M={M} N={N} K={K} {fa}x{fb} act={act} sb={nsb}",
+                       acc=2.0 ** -15)
     return rel
 
 
@@ -245,6 +309,13 @@ def test_fp8_gemm_wide_tiles(R, M, N, K, fa, fb):
     rng = np.random.default_rng(M + N + K + 4 * fa + fb)
     for act, nsb in (("pcs", "N"), ("unit", "1"), ("pcs", "0")):
         check_fp8(R, rng, M, N, K, fa, fb, act, nsb, sample_cols=96)
+
+
+def test_fp8_gemm_every_output_of_a_qwen_32b_projection(R):
+    """Every output of the M = 1024 prefill product on Qwen2.5-32B's q/o shape
+    [5120, 5120], each element against float64 numpy."""
+    rng = np.random.default_rng(131)
+    check_fp8(R, rng, 1024, 5120, 5120, E4M3, E4M3)
 
 
 @pytest.mark.parametrize("shape", [(5120, 5120), (1024, 5120), (27648, 5120), (5120, 27648)])

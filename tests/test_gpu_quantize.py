@@ -351,3 +351,43 @@ def test_the_f32_2048x2048_workload(R, fmt):
     x[idx] *= np.float32(50.0)
     for sc in ("pcs", "hw", "unit"):
         check_quantize(R, x, rows, cols, fmt, sc, label=f"f32 2048x2048 {sc}")
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_rows_whose_scale_is_subnormal(R, fmt):
+    """bf16 rows whose absmax is a bf16 subnormal (2^-133 .. 2^-127): s = m / max
+    is an f32 subnormal with few significant bits (E5M2, m = 2^-133: s rounds
+    to 2^-149 and x / s reaches 2^16, past 57344), so the quotient passes the
+    range the clamp-free conversion covers; such rows must still saturate as
+    the reference does. Both fast-path widths and a generic one."""
+    rng = np.random.default_rng(61 + fmt)
+    for rows, cols in [(64, 4096), (32, 14336), (16, 100)]:
+        w = np.zeros((rows, cols), dtype=np.uint16)
+        for r in range(rows):
+            top = 1 + (r % 64)   # absmax bit pattern 0x0001 .. 0x0040
+            vals = rng.integers(0, top + 1, cols).astype(np.uint16)
+            vals |= (rng.integers(0, 2, cols).astype(np.uint16) << 15)
+            vals[0] = top
+            w[r] = vals
+        for backoff in (1.0, 0.5):
+            check_quantize(R, w.ravel(), rows, cols, fmt, "pcs", backoff, label=f"tiny bf16 {rows}x{cols} b{backoff}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_the_staged_host_entry_over_many_chunks(R, dtype):
+    """reng_hip_quantize_host moves a matrix in pinned row chunks over two
+    streams: matrices of 1, several and a ragged number of chunks (16 MB of
+    input each), every scheme, bit for bit against the oracle, twice in a row
+    (the staging buffers are kept and reused)."""
+    rng = np.random.default_rng(71)
+    for rows, cols in [(64, 4096), (4100, 4096), (2304, 14336)]:
+        x = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        w = bf16_bits(x).ravel() if dtype == "bf16" else x.ravel()
+        for fmt, sc in ((E4M3, "pcs"), (E5M2, "hw"), (E4M3, "unit"), (E4M3, "hw")):
+            for _ in range(2):
+                codes, scales, eb = R.quantize_host(w, rows, cols, fmt, sc, 0.8)
+                ref = O.quantize_with(w, rows, cols, fmt, sc, 0.8)
+                assert eb == ref.exp_bias, (rows, cols, fmt, sc)
+                assert np.array_equal(scales.view(np.uint32), ref.scales.view(np.uint32)), (rows, cols, fmt, sc)
+                bad = np.nonzero(codes != ref.codes)[0]
+                assert bad.size == 0, (rows, cols, fmt, sc, bad[:4])

@@ -461,3 +461,25 @@ def test_f32_quantize_a_planted_mistake_is_caught():
     assert np.array_equal(O.quantize_with(x.ravel(), rows, cols, E4M3, "pcs").codes, codes)
     recip = nearest_encode((x * (np.float32(1.0) / s2)[:, None]).astype(np.float32), E4M3)
     assert not np.array_equal(recip, codes)
+
+
+def test_rows_whose_scale_is_subnormal_saturate():
+    """The closed form on bf16 rows of absmax 2^-133 .. 2^-127: E5M2's s rounds
+    to a subnormal with few bits, the quotient passes 57344 and saturates."""
+    rng = np.random.default_rng(67)
+    rows, cols = 64, 256
+    w = np.zeros((rows, cols), dtype=np.uint16)
+    for r in range(rows):
+        top = 1 + r
+        w[r] = rng.integers(0, top + 1, cols).astype(np.uint16) | (rng.integers(0, 2, cols).astype(np.uint16) << 15)
+        w[r, 0] = top
+    x = bf16_f32(w)
+    for fmt in (E4M3, E5M2):
+        from helpers import quantize_f32_closed_form
+
+        codes, s, _ = quantize_f32_closed_form(x.reshape(rows, cols), fmt, "pcs", 1.0)
+        q = O.quantize(w.ravel(), rows, cols, fmt, "pcs")
+        assert np.array_equal(q.scales.view(np.uint32), s.view(np.uint32))
+        assert np.array_equal(q.codes, codes)
+    q = O.quantize(w.ravel(), rows, cols, E5M2, "pcs")
+    assert q.scales[0] == np.float32(2.0 ** -149) and q.codes[0] == 0x7B   # x / s = 2^16 saturates
