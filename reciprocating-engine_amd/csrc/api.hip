@@ -468,6 +468,19 @@ RENG_HIP_API int reng_hip_stream_read(const void *p, size_t bytes, void *sink, v
     return launch_stream_read(p, bytes, static_cast<uint32_t *>(sink), as_stream(stream));
 }
 
+RENG_HIP_API int reng_hip_gemm_w8a16_noalloc(const uint16_t *x, const uint8_t *codes, const float *scales,
+                                             size_t M, size_t N, size_t K, int format, uint16_t *y,
+                                             void *stream) {
+    clear_error();
+    if (int rc = w8a16_args(x, codes, M, N, K, format, y)) return rc;
+    int rc = RENG_HIP_OK;
+    float *p = static_split_scratch(&rc);   // resolved once per device, on its first call there
+    if (rc) return rc;
+    const SplitScratch fixed{p, STATIC_SCRATCH_FLOATS};
+    return launch_w8a16(x, codes, scales, (uint32_t)M, (uint32_t)N, (uint32_t)K, format, y,
+                        as_stream(stream), &fixed);
+}
+
 namespace {
 
 int gemv_epi_args(const uint16_t *x, const uint8_t *codes, size_t N, size_t K, int format) {

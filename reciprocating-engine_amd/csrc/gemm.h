@@ -7,8 +7,21 @@
 
 namespace reng {
 
+// Where a launch keeps its split-K partials: fixed == nullptr takes the
+// library's grow-only per-stream buffer (split_workspace, which may allocate);
+// otherwise the `floats` floats at ptr, and a plan that needs more is refused.
+struct SplitScratch {
+    float *ptr;
+    size_t floats;
+};
+
 int launch_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
-                 uint32_t N, uint32_t K, int format, uint16_t *y, hipStream_t st);
+                 uint32_t N, uint32_t K, int format, uint16_t *y, hipStream_t st,
+                 const SplitScratch *fixed = nullptr);
+// The per-device address of the library's static split-K scratch array
+// (STATIC_SCRATCH_FLOATS floats), looked up once per device; sets *rc.
+constexpr size_t STATIC_SCRATCH_FLOATS = (size_t)4 << 20;   // 16 MiB
+float *static_split_scratch(int *rc);
 // M = 1 with a fused epilogue: f32 y[n] = res[n] + bf16((W x)[n]) (residual), or
 // over rows in (gate, up) pairs, y[i] = bf16(silu(bf16 (W x)[2i]) * bf16 (W x)[2i + 1]) (N even).
 int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
@@ -29,11 +42,14 @@ int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *sca
                        uint32_t K, int format, uint16_t *y, hipStream_t st);
 // 16 < M <= 64 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                       uint32_t K, int format, uint16_t *y, hipStream_t st);
+                       uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed);
 // A grow-only f32 workspace of at least `floats` for split-K partials, one per
 // (device, stream) (csrc/gemm.hip); sets *rc. It refuses to grow while the
 // stream is being captured into a graph.
 float *split_workspace(size_t floats, hipStream_t st, int *rc);
+// The partials of a launch: from `fixed` when given (refusing a plan that
+// needs more than it holds), else from split_workspace.
+float *split_partials(size_t floats, hipStream_t st, const SplitScratch *fixed, int *rc);
 // The read yardstick: bytes / 1024 whole 1 KB chunks of p read once; sink
 // holds stream_read_sink_words() words (written only by chance).
 int launch_stream_read(const void *p, size_t bytes, uint32_t *sink, hipStream_t st);

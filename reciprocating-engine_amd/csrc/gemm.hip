@@ -530,7 +530,8 @@ uint32_t stream_read_sink_words() { return (uint32_t)device_props().cus * 8; }
 // stream destroyed while its work is still queued must not have its handle
 // reused by another before that work ends). Growing it synchronizes the stream
 // and calls hipMalloc, which a stream under graph capture cannot do: that case
-// is refused (warm the stream up with the largest product first).
+// is refused (warm the stream up with the largest product first, or use the
+// allocation-free entry point).
 float *split_workspace(size_t floats, hipStream_t st, int *rc) {
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, std::pair<float *, size_t>> bufs;
@@ -542,7 +543,7 @@ float *split_workspace(size_t floats, hipStream_t st, int *rc) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
             set_error("the split-K workspace would grow to %zu bytes while the stream is captured: run the "
-                      "product once on this stream before capturing",
+                      "product once on this stream before capturing, or call reng_hip_gemm_w8a16_noalloc",
                       floats * sizeof(float));
             *rc = RENG_HIP_EINVAL;
             return nullptr;
@@ -571,6 +572,51 @@ float *split_workspace(size_t floats, hipStream_t st, int *rc) {
     }
     *rc = RENG_HIP_OK;
     return e.first;
+}
+
+// The allocation-free entry point's partials: a static array in device memory,
+// one copy per device (the code object's), whose address each device resolves
+// once with hipGetSymbolAddress. In host code `scratch` names a host-side
+// stand-in, never the device memory: only the looked-up address is passed on.
+static __device__ __align__(256) float scratch[STATIC_SCRATCH_FLOATS];
+
+float *static_split_scratch(int *rc) {
+    static std::mutex mu;
+    static std::map<int, float *> addr;
+    int dev = 0;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess) {
+        set_error("hipGetDevice: %s", hipGetErrorString(ge));
+        *rc = RENG_HIP_EDEVICE;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = addr.find(dev);
+    if (it == addr.end()) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+            *rc = RENG_HIP_EDEVICE;
+            return nullptr;
+        }
+        it = addr.emplace(dev, static_cast<float *>(p)).first;
+    }
+    *rc = RENG_HIP_OK;
+    return it->second;
+}
+
+float *split_partials(size_t floats, hipStream_t st, const SplitScratch *fixed, int *rc) {
+    if (!fixed) return split_workspace(floats, st, rc);
+    if (floats > fixed->floats) {
+        set_error("this product's split-K plan needs %zu bytes of scratch; the static scratch holds %zu "
+                  "(reng_hip_gemm_w8a16 allocates what it needs)",
+                  floats * sizeof(float), fixed->floats * sizeof(float));
+        *rc = RENG_HIP_EINVAL;
+        return nullptr;
+    }
+    *rc = RENG_HIP_OK;
+    return fixed->ptr;
 }
 
 // The GEMV's launch for M <= 4 rows: rows (or row groups of `unit`, which a
@@ -729,7 +775,7 @@ int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scale
 
 template <int F>
 int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
-                   uint32_t N, uint32_t K, uint16_t *y, hipStream_t st) {
+                   uint32_t N, uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     // One activation row: the contiguous-rows GEMV while the row fits in LDS
     // (64 KB); x and codes are 16-byte aligned (checked by the entry point).
     if (M == 1 && K <= 32768)
@@ -740,7 +786,7 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
         for (uint32_t mb = 0; mb < M; mb += 4) {
             const uint32_t mt = M - mb < 4 ? M - mb : 4;
             const int rc = launch_w8a16_t<F>(x + (size_t)mb * K, codes, scales, mt, N, K,
-                                             y + (size_t)mb * N, st);
+                                             y + (size_t)mb * N, st, fixed);
             if (rc) return rc;
         }
         return RENG_HIP_OK;
@@ -781,16 +827,17 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     for (uint32_t mb = 0; mb < M; mb += 64) {
         const uint32_t mt = M - mb < 64 ? M - mb : 64;
         const int rc = mt <= 16 ? launch_skinny_mfma(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st)
-                                : launch_skinny_wide(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st);
+                                : launch_skinny_wide(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st,
+                                                     fixed);
         if (rc) return rc;
     }
     return RENG_HIP_OK;
 }
 
 int launch_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
-                 uint32_t N, uint32_t K, int format, uint16_t *y, hipStream_t st) {
-    return format == RENG_HIP_E4M3 ? launch_w8a16_t<RENG_HIP_E4M3>(x, codes, scales, M, N, K, y, st)
-                                   : launch_w8a16_t<RENG_HIP_E5M2>(x, codes, scales, M, N, K, y, st);
+                 uint32_t N, uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
+    return format == RENG_HIP_E4M3 ? launch_w8a16_t<RENG_HIP_E4M3>(x, codes, scales, M, N, K, y, st, fixed)
+                                   : launch_w8a16_t<RENG_HIP_E5M2>(x, codes, scales, M, N, K, y, st, fixed);
 }
 
 }  // namespace reng

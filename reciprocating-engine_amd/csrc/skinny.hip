@@ -566,7 +566,7 @@ __global__ __launch_bounds__(64) void reduce_splits(const float *__restrict__ pa
 // ring takes 128-144 KB of LDS).
 template <int F, int MT, int NTW, int S>
 int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                    uint32_t K, uint16_t *y, hipStream_t st) {
+                    uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     const uint32_t tiles = (N + 32 * NTW - 1) / (32 * NTW);
     const uint32_t chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
     // At least 4 chunks (512 codes) per split: below that the partials
@@ -577,7 +577,7 @@ int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales
     const uint32_t cps = (chunks + splits - 1) / splits;
     splits = (chunks + cps - 1) / cps;
     int rc = RENG_HIP_OK;
-    float *part = splits > 1 ? split_workspace((size_t)splits * M * N, st, &rc) : nullptr;
+    float *part = splits > 1 ? split_partials((size_t)splits * M * N, st, fixed, &rc) : nullptr;
     if (rc) return rc;
     hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S>), dim3(tiles, splits), dim3(256), 0, st, x, codes, scales, M, N,
                        K, cps, y, part);
@@ -600,26 +600,26 @@ inline uint32_t wide_blocks(uint32_t N, uint32_t K, uint32_t R) {
 
 template <int F, int MT>
 int launch_wide_mt(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                   uint32_t K, uint16_t *y, hipStream_t st) {
+                   uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     // 64-row blocks for small matrices (fewer splits: the partials cost more
     // than the activation re-reads there), else 128 (half the activation
     // bytes per code) - unless 128-row blocks leave over 30% of the CUs idle
     // and 96-row ones cover more (Qwen2.5-7B gate/up [18944, 3584]: 148 ->
     // 198 blocks, M = 64: 26.8 -> 24.1 us).
-    if ((uint64_t)N * K <= (16ull << 20)) return launch_wide_cfg<F, MT, 2, 6>(x, codes, scales, M, N, K, y, st);
+    if ((uint64_t)N * K <= (16ull << 20)) return launch_wide_cfg<F, MT, 2, 6>(x, codes, scales, M, N, K, y, st, fixed);
     const uint32_t cus = (uint32_t)device_props().cus, b128 = wide_blocks(N, K, 128);
     if (10 * b128 < 7 * cus && wide_blocks(N, K, 96) > b128)
-        return launch_wide_cfg<F, MT, 3, 3>(x, codes, scales, M, N, K, y, st);
-    return launch_wide_cfg<F, MT, 4, 4>(x, codes, scales, M, N, K, y, st);
+        return launch_wide_cfg<F, MT, 3, 3>(x, codes, scales, M, N, K, y, st, fixed);
+    return launch_wide_cfg<F, MT, 4, 4>(x, codes, scales, M, N, K, y, st, fixed);
 }
 
 template <int F>
 int launch_wide_f(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                  uint32_t K, uint16_t *y, hipStream_t st) {
+                  uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     switch ((M + 15) / 16) {
-        case 2: return launch_wide_mt<F, 2>(x, codes, scales, M, N, K, y, st);
-        case 3: return launch_wide_mt<F, 3>(x, codes, scales, M, N, K, y, st);
-        default: return launch_wide_mt<F, 4>(x, codes, scales, M, N, K, y, st);
+        case 2: return launch_wide_mt<F, 2>(x, codes, scales, M, N, K, y, st, fixed);
+        case 3: return launch_wide_mt<F, 3>(x, codes, scales, M, N, K, y, st, fixed);
+        default: return launch_wide_mt<F, 4>(x, codes, scales, M, N, K, y, st, fixed);
     }
 }
 
@@ -639,10 +639,10 @@ int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *sca
 
 // 16 < M <= 64, K % 128 == 0.
 int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                       uint32_t K, int format, uint16_t *y, hipStream_t st) {
+                       uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     using namespace skinny;
-    if (format == RENG_HIP_E4M3) return launch_wide_f<RENG_HIP_E4M3>(x, codes, scales, M, N, K, y, st);
-    return launch_wide_f<RENG_HIP_E5M2>(x, codes, scales, M, N, K, y, st);
+    if (format == RENG_HIP_E4M3) return launch_wide_f<RENG_HIP_E4M3>(x, codes, scales, M, N, K, y, st, fixed);
+    return launch_wide_f<RENG_HIP_E5M2>(x, codes, scales, M, N, K, y, st, fixed);
 }
 
 }  // namespace reng

@@ -57,6 +57,7 @@ SIGNATURES = {
     "reng_hip_dequantize": (_I, [_P, _P, _SZ, _SZ, _I, _I, _P, _P]),
     "reng_hip_row_errors": (_I, [_P, _P, _P, _SZ, _SZ, _I, _SZ, _P, _P, _P]),
     "reng_hip_gemm_w8a16": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _I, _P, _P]),
+    "reng_hip_gemm_w8a16_noalloc": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _I, _P, _P]),
     "reng_hip_gemm_fp8_scaled": (_I, [_P, _I, _P, _SZ, _P, _I, _P, _SZ, _SZ, _SZ, _SZ, _P, _P]),
     "reng_hip_verify_hw_convert": (_I, [_I, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32)]),
     "reng_hip_rms_norm_bf16": (_I, [_P, _P, _SZ, _SZ, _F, _P, _P]),
