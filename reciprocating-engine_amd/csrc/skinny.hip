@@ -605,12 +605,16 @@ int launch_wide_mt(const uint16_t *x, const uint8_t *codes, const float *scales,
     // than the activation re-reads there), else 128 (half the activation
     // bytes per code) - unless 128-row blocks leave over 30% of the CUs idle
     // and 96-row ones cover more (Qwen2.5-7B gate/up [18944, 3584]: 148 ->
-    // 198 blocks, M = 64: 26.8 -> 24.1 us).
-    if ((uint64_t)N * K <= (16ull << 20)) return launch_wide_cfg<F, MT, 2, 6>(x, codes, scales, M, N, K, y, st, fixed);
+    // 198 blocks, M = 64: 26.8 -> 24.1 us). Ring depths from a sweep of 3-6
+    // stages per form on MI355X (Qwen2.5-7B shapes, M = 32 and 64): 4 stages
+    // for the 64- and 96-row forms (M = 64 [3584, 3584] 12.8 -> 11.6 us,
+    // [18944, 3584] 24.2 -> 22.9 us; M = 32 [18944, 3584] 20.7 -> 17.6 us),
+    // 3 for the 128-row one ([3584, 18944] 23.8 -> 22.4 us).
+    if ((uint64_t)N * K <= (16ull << 20)) return launch_wide_cfg<F, MT, 2, 4>(x, codes, scales, M, N, K, y, st, fixed);
     const uint32_t cus = (uint32_t)device_props().cus, b128 = wide_blocks(N, K, 128);
     if (10 * b128 < 7 * cus && wide_blocks(N, K, 96) > b128)
-        return launch_wide_cfg<F, MT, 3, 3>(x, codes, scales, M, N, K, y, st, fixed);
-    return launch_wide_cfg<F, MT, 4, 4>(x, codes, scales, M, N, K, y, st, fixed);
+        return launch_wide_cfg<F, MT, 3, 4>(x, codes, scales, M, N, K, y, st, fixed);
+    return launch_wide_cfg<F, MT, 4, 3>(x, codes, scales, M, N, K, y, st, fixed);
 }
 
 template <int F>
