@@ -251,6 +251,27 @@ def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3", read_yardstick=False):
     return rec
 
 
+def bench_w8a16_tiles(torch, R, gen):
+    """More than 64 activation rows (the tiled bf16-MFMA kernel): M = 256 on the
+    reference probe's timed shapes (fp8_probe.rs:359-431) and M = 1024 on the
+    Qwen2.5-32B prefill shapes, each beside a bf16 x bf16 torch.matmul
+    (hipBLASLt) over the dequantized weight as the library yardstick."""
+    out = []
+    for M, N, K in ((256, 4096, 4096), (256, 14336, 4096), (1024, 5120, 5120), (1024, 27648, 5120),
+                    (1024, 5120, 27648)):
+        rec = bench_w8a16(torch, R, gen, M, N, K)
+        wb = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+        wt = wb.t().contiguous()
+        del wb
+        x = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16)
+        secs = graph_time(torch, lambda i: torch.matmul(x, wt), 10)
+        rec["bf16_matmul_us"] = round(secs * 1e6, 2)
+        out.append(rec)
+        del wt, x
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_fp8_gemm(torch, R, gen, M, N, K):
     w = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16).view(-1)
     qw = R.quantize_with(w, N, K, "e4m3", "pcs")
@@ -469,7 +490,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--part", default="all",
-                    choices=["all", "quantize", "gemv", "skinny", "prefill", "f32", "decode", "qwen32b", "host"],
+                    choices=["all", "quantize", "gemv", "skinny", "tiles", "prefill", "f32", "decode", "qwen32b",
+                             "host"],
                     help="run one part only (for profiling); the JSON line is printed for 'all' and 'quantize'")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy 1 GiB device-to-device three times first: a kernel of known traffic that "
@@ -508,6 +530,8 @@ def main():
             out = [bench_host_quantize(torch, R)]
         elif args.part == "skinny":
             out = [bench_w8a16(torch, R, gen, M, N, K) for M in (8, 64) for _, N, K in QWEN_7B]
+        elif args.part == "tiles":
+            out = bench_w8a16_tiles(torch, R, gen)
         elif args.part == "prefill":
             out = [bench_fp8_gemm(torch, R, gen, 1024, N, K) for N, K in ((5120, 5120), (1024, 5120),
                                                                            (27648, 5120), (5120, 27648))]
@@ -570,6 +594,8 @@ def main():
         extras["skinny_qwen7b"] = sk
         log("skinny:", sk)
         torch.cuda.empty_cache()
+        extras["w8a16_tiles"] = bench_w8a16_tiles(torch, R, gen)
+        log("w8a16 tiles:", extras["w8a16_tiles"])
         extras["prefill_fp8_m1024_qwen32b"] = [bench_fp8_gemm(torch, R, gen, 1024, N, K)
                                                for N, K in ((5120, 5120), (1024, 5120), (27648, 5120),
                                                             (5120, 27648))]

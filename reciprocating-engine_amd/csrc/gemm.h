@@ -43,6 +43,12 @@ int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *sca
 // 16 < M <= 64 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed);
+// More than 64 activation rows, K % 64 == 0, on whole output tiles
+// (csrc/gemm_tiles.hip). w8a16_tiles_take says whether the tiled kernel takes
+// the product (enough tiles for the chip; otherwise the 64-row kernels loop).
+bool w8a16_tiles_take(uint32_t M, uint32_t N, uint32_t K);
+int launch_w8a16_tiles(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
+                       uint32_t K, int format, uint16_t *y, hipStream_t st);
 // A grow-only f32 workspace of at least `floats` for split-K partials, one per
 // (device, stream) (csrc/gemm.hip); sets *rc. It refuses to grow while the
 // stream is being captured into a graph.

@@ -225,6 +225,31 @@ def test_skinny_every_output_of_a_qwen_7b_gate_up(R, M):
     check_w8a16(R, rng, M, 18944, 3584, E4M3)
 
 
+@pytest.mark.parametrize("M, N, K, fmt", [
+    (1024, 16384, 128, E4M3),   # 256 x 256 tiles (one per CU)
+    (512, 8192, 192, E5M2),     # 128 x 256 tiles; K % 128 != 0
+    (256, 12288, 256, E4M3),    # 128 x 128 tiles, six stages
+    (200, 4097, 320, E5M2),     # 64 x 128 tiles; ragged M and N (element stores)
+])
+def test_w8a16_tiles_every_output(R, M, N, K, fmt):
+    """More than 64 activation rows take the tiled bf16-MFMA kernel; one shape
+    per tile size the launcher picks on a 256-CU MI355X, every output against
+    the oracle and float64."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    check_w8a16(R, rng, M, N, K, fmt)
+
+
+def test_w8a16_tiles_two_input_form(R):
+    """No scale operand on the tiled kernel: the product over the raw codes."""
+    rng = np.random.default_rng(5)
+    M, N, K = 256, 8192, 64
+    q = quantized_weight(rng, N, K, E4M3)
+    x = bf16_bits(rng.standard_normal((M, K)).astype(np.float32)).ravel()
+    y = bf16_out(R.gemm_w8a16(dev(x), dev(q.codes), None, M, N, K, E4M3)).reshape(M, N)
+    raw = O.decode_array(q.codes, E4M3).reshape(N, K)
+    assert_elementwise(y, bf16_f32(x), raw, K, "tiles, no scales")
+
+
 def test_the_reference_probe_shapes(R):
     """fp8_probe.rs:478-505: weights(512, 256), m in {1, 256}, rel_L2 < 0.02."""
     N, K = 512, 256
