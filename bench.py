@@ -253,12 +253,13 @@ def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3", read_yardstick=False):
 
 def bench_w8a16_tiles(torch, R, gen):
     """More than 64 activation rows (the tiled bf16-MFMA kernel): M = 256 on the
-    reference probe's timed shapes (fp8_probe.rs:359-431) and M = 1024 on the
+    reference probe's timed shapes (fp8_probe.rs:359-431), the Llama-3.1-8B
+    down projection (long K: stream-K) and M = 1024 on the
     Qwen2.5-32B prefill shapes, each beside a bf16 x bf16 torch.matmul
     (hipBLASLt) over the dequantized weight as the library yardstick."""
     out = []
-    for M, N, K in ((256, 4096, 4096), (256, 14336, 4096), (1024, 5120, 5120), (1024, 27648, 5120),
-                    (1024, 5120, 27648)):
+    for M, N, K in ((256, 4096, 4096), (256, 14336, 4096), (256, 4096, 14336), (1024, 5120, 5120),
+                    (1024, 27648, 5120), (1024, 5120, 27648)):
         rec = bench_w8a16(torch, R, gen, M, N, K)
         wb = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
         wt = wb.t().contiguous()

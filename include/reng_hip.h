@@ -157,13 +157,14 @@ RENG_HIP_API int reng_hip_gemm_w8a16(const uint16_t *x, const uint8_t *codes, co
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc. Same arguments, kernels and results (bit for bit) as
  * reng_hip_gemm_w8a16; the split-K partials of 16 < M <= 64 products (and of
- * each 64-row tile of a larger M) go to a static 16 MiB array in device memory
- * that the library holds on each GPU it runs on until the process ends,
- * instead of the grow-only per-stream buffer reng_hip_gemm_w8a16 allocates. A
- * product whose split plan needs more than 16 MiB is refused (EINVAL); on a
- * 256-CU device the plans need at most 8.4 MiB. Every call on one GPU shares
- * that GPU's array, so calls that overlap on one GPU race: order them on one
- * stream (or otherwise serialize them). */
+ * each 64-row tile of a larger M) and the stream-K partials of long-K M > 64
+ * products go to a static 32 MiB array in device memory, and the stream-K
+ * tile counters to a static array of 4096 counters, that the library holds on
+ * each GPU it runs on until the process ends, instead of the grow-only
+ * per-stream buffers reng_hip_gemm_w8a16 allocates. A product whose plan needs
+ * more is refused (EINVAL); on a 256-CU device the plans need at most 24 MiB.
+ * Every call on one GPU shares that GPU's arrays, so calls that overlap on one
+ * GPU race: order them on one stream (or otherwise serialize them). */
 RENG_HIP_API int reng_hip_gemm_w8a16_noalloc(const uint16_t *x, const uint8_t *codes, const float *scales,
                                              size_t M, size_t N, size_t K, int format, uint16_t *y,
                                              void *stream);

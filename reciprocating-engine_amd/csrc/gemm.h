@@ -20,7 +20,7 @@ int launch_w8a16(const uint16_t *x, const uint8_t *codes, const float *scales, u
                  const SplitScratch *fixed = nullptr);
 // The per-device address of the library's static split-K scratch array
 // (STATIC_SCRATCH_FLOATS floats), looked up once per device; sets *rc.
-constexpr size_t STATIC_SCRATCH_FLOATS = (size_t)4 << 20;   // 16 MiB
+constexpr size_t STATIC_SCRATCH_FLOATS = (size_t)8 << 20;   // 32 MiB
 float *static_split_scratch(int *rc);
 // M = 1 with a fused epilogue: f32 y[n] = res[n] + bf16((W x)[n]) (residual), or
 // over rows in (gate, up) pairs, y[i] = bf16(silu(bf16 (W x)[2i]) * bf16 (W x)[2i + 1]) (N even).
@@ -48,7 +48,13 @@ int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *sca
 // the product (enough tiles for the chip; otherwise the 64-row kernels loop).
 bool w8a16_tiles_take(uint32_t M, uint32_t N, uint32_t K);
 int launch_w8a16_tiles(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                       uint32_t K, int format, uint16_t *y, hipStream_t st);
+                       uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed);
+// Zeroed stream-K tile counters (every launch leaves them zeroed): a grow-only
+// buffer per (device, stream), or the library's static array
+// (STATIC_TILE_COUNTERS of them per device) for callers that cannot allocate.
+constexpr uint32_t STATIC_TILE_COUNTERS = 4096;
+uint32_t *tile_counters(uint32_t count, hipStream_t st, int *rc);
+uint32_t *static_tile_counters(int *rc);
 // A grow-only f32 workspace of at least `floats` for split-K partials, one per
 // (device, stream) (csrc/gemm.hip); sets *rc. It refuses to grow while the
 // stream is being captured into a graph.

@@ -606,6 +606,82 @@ float *static_split_scratch(int *rc) {
     return it->second;
 }
 
+// Stream-K tile counters: zeroed when allocated, and every launch that uses
+// them leaves them zeroed (the last block of each split tile resets its
+// counter). One grow-only buffer per (device, stream), as split_workspace.
+uint32_t *tile_counters(uint32_t count, hipStream_t st, int *rc) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, std::pair<uint32_t *, uint32_t>> bufs;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(mu);
+    auto &e = bufs[{dev, st}];
+    if (e.second < count) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+            set_error("the stream-K tile counters would grow to %u while the stream is captured: run the product "
+                      "once on this stream before capturing",
+                      count);
+            *rc = RENG_HIP_EINVAL;
+            return nullptr;
+        }
+        if (e.first) {
+            const hipError_t se = hipStreamSynchronize(st);
+            if (se != hipSuccess) {
+                set_error("hipStreamSynchronize: %s", hipGetErrorString(se));
+                *rc = RENG_HIP_EDEVICE;
+                return nullptr;
+            }
+            (void)hipFree(e.first);
+            e.first = nullptr;
+            e.second = 0;
+        }
+        void *p = nullptr;
+        hipError_t ae = hipMalloc(&p, (size_t)count * sizeof(uint32_t));
+        if (ae == hipSuccess) ae = hipMemset(p, 0, (size_t)count * sizeof(uint32_t));
+        if (ae != hipSuccess) {
+            if (p) (void)hipFree(p);
+            set_error("tile counters (%u): %s", count, hipGetErrorString(ae));
+            *rc = RENG_HIP_ENOMEM;
+            return nullptr;
+        }
+        e.first = static_cast<uint32_t *>(p);
+        e.second = count;
+    }
+    *rc = RENG_HIP_OK;
+    return e.first;
+}
+
+// The allocation-free entry point's tile counters: zero from load, left zeroed
+// by every launch, one copy per device (resolved as `scratch` is).
+static __device__ __align__(256) uint32_t counters[STATIC_TILE_COUNTERS];
+
+uint32_t *static_tile_counters(int *rc) {
+    static std::mutex mu;
+    static std::map<int, uint32_t *> addr;
+    int dev = 0;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess) {
+        set_error("hipGetDevice: %s", hipGetErrorString(ge));
+        *rc = RENG_HIP_EDEVICE;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = addr.find(dev);
+    if (it == addr.end()) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(counters));
+        if (e != hipSuccess || !p) {
+            set_error("hipGetSymbolAddress(counters) on device %d: %s", dev, hipGetErrorString(e));
+            *rc = RENG_HIP_EDEVICE;
+            return nullptr;
+        }
+        it = addr.emplace(dev, static_cast<uint32_t *>(p)).first;
+    }
+    *rc = RENG_HIP_OK;
+    return it->second;
+}
+
 float *split_partials(size_t floats, hipStream_t st, const SplitScratch *fixed, int *rc) {
     if (!fixed) return split_workspace(floats, st, rc);
     if (floats > fixed->floats) {
@@ -784,7 +860,7 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     // once per 64-256 activation rows (the 64-row loop below re-reads every
     // code once per 64 rows: M = 256 [14336, 4096] 86.8 -> 41.6 us).
     if (M > 64 && K % 64 == 0 && w8a16_tiles_take(M, N, K))
-        return launch_w8a16_tiles(x, codes, scales, M, N, K, F, y, st);
+        return launch_w8a16_tiles(x, codes, scales, M, N, K, F, y, st, fixed);
     if (M > 4 && K % 128 != 0) {
         // The MFMA kernel walks K in 128-code chunks; other widths take the
         // GEMV kernel four activation rows at a time.

@@ -239,6 +239,20 @@ def test_w8a16_tiles_every_output(R, M, N, K, fmt):
     check_w8a16(R, rng, M, N, K, fmt)
 
 
+@pytest.mark.parametrize("M, N, K, fmt", [
+    (256, 2048, 8192, E4M3),    # 32 tiles of 128 x 128 over 64 stages each: stream-K
+    (200, 1000, 8320, E5M2),    # ragged M and N under stream-K
+])
+def test_w8a16_stream_k_every_output(R, M, N, K, fmt):
+    """Long K over few tiles runs stream-K: blocks take equal runs of
+    (tile, stage) units across tile edges and the last block of each split tile
+    adds the partials. Two products in a row with other weights check that the
+    tile counters come back to zero."""
+    rng = np.random.default_rng(M + N + K)
+    check_w8a16(R, rng, M, N, K, fmt)
+    check_w8a16(R, rng, M, N, K, fmt)
+
+
 def test_w8a16_tiles_two_input_form(R):
     """No scale operand on the tiled kernel: the product over the raw codes."""
     rng = np.random.default_rng(5)

@@ -2,7 +2,8 @@
 the C ABI it must give what reng_hip_gemm_w8a16 gives, bit for bit, on two
 calls in a row (the second smaller, so it runs on what the first left in the
 shared static scratch), on products that use the split-K scratch (16 < M <= 64
-with K splits, M > 64 in 64-row tiles) and on ones that do not."""
+with K splits, M > 64 in 64-row tiles), the stream-K partials and tile
+counters (long-K M > 64 over few tiles) and on ones that do not."""
 import ctypes
 
 import numpy as np
@@ -48,6 +49,7 @@ def call(R, name, x, codes, scales, M, N, K, fmt):
     ((64, 3584, 18944), (17, 1000, 1024)),    # the largest Qwen2.5-7B plan, then a 2-tile one
     ((130, 2048, 1024), (65, 700, 512)),      # M > 64: 64-row tiles share the scratch in stream order
     ((8, 18944, 3584), (1, 4096, 4096)),      # no split: skinny_rows, then the GEMV
+    ((256, 2048, 8192), (100, 1000, 8192)),   # stream-K partials and counters, then a smaller stream-K plan
 ])
 def test_noalloc_matches_the_allocating_entry_twice(R, first, second):
     rng = np.random.default_rng(sum(first) + sum(second))
