@@ -171,14 +171,21 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma(const uint8_t *__restrict__
             interleave<WM * WN, 2 * (WM + WN), 0>();
             __builtin_amdgcn_sched_barrier(0);
         } else {
-            mfma_rows(0, WM / 2, fa[CUR], fb[CUR]);
-            __builtin_amdgcn_sched_barrier(0);
+            // This k-step's fragments (the stage's last) are in registers once
+            // the wave's LDS reads are done; after the barrier no wave reads
+            // stage t's slot again, so the copy of stage t + S goes there, and
+            // stage t + 1 (landed: the vmcnt wait) is read during all of this
+            // k-step's MFMAs. The reads come before the copies in program
+            // order: they are needed a k-step earlier, and the compiler keeps
+            // LDS reads and LDS-bound copies in order.
+            wait_lgkm0();
             wait_vmcnt<(S - 2) * T::LOADS>();
             lds_barrier();
             issue(clampi(t + S), (int)(t % S));
             read_frags((int)((t + 1) % S), 0, fa[NXT], fb[NXT]);
-            mfma_rows(WM / 2, WM, fa[CUR], fb[CUR]);
-            interleave<WM / 2 * WN, 2 * (WM + WN), T::LOADS>();
+            mfma_rows(0, WM, fa[CUR], fb[CUR]);
+            __builtin_amdgcn_sched_group_barrier(0x060, T::LOADS, 0);
+            interleave<WM * WN, 2 * (WM + WN), 0>();
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -203,12 +210,15 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma(const uint8_t *__restrict__
     // m = l % 32 (activation row) and rows n = 8 (e / 4) + 4 (l / 32) + e % 4,
     // so each group of four e is four consecutive outputs of row m: one 8-byte
     // store.
+    // Scales as (pointer, stride), as in gemm_fp8_wide: no branches on the scale form.
+    const float *sap = nsa == 0 ? &one_f32 : sa, *sbp = nsb == 0 ? &one_f32 : sb;
+    const uint32_t sas = nsa > 1, sbs = nsb > 1;
     auto store = [&](const f32x16 (&v)[WM][WN]) {
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
             const uint32_t m = m0 + wm * (BM / 2) + i * 32 + rl;
             if (m >= M) continue;
-            const float sam = nsa == 0 ? 1.0f : (nsa == 1 ? sa[0] : sa[m]);
+            const float sam = sap[m * sas];
             uint16_t *orow = out + (size_t)m * N;
 #pragma unroll
             for (int j = 0; j < WN; ++j)
@@ -219,8 +229,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma(const uint8_t *__restrict__
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const uint32_t nn = nb + e < N ? nb + e : N - 1;
-                        const float sbn = nsb == 0 ? 1.0f : (nsb == 1 ? sb[0] : sb[nn]);
-                        o[e] = v[i][j][4 * g + e] * sam * sbn;
+                        o[e] = v[i][j][4 * g + e] * sam * sbp[nn * sbs];
                     }
                     if (vec_out && nb + 3 < N) {
                         const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
@@ -289,25 +298,26 @@ __device__ __forceinline__ void copy16_buf(__amdgpu_buffer_rsrc_t r, uint8_t *l,
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)l, 16, voff, soff, 0, 0);
 }
 
-template <int WM, int WN>
+template <int WM, int WN, int BK_ = 128>
 struct WideTile {
     static constexpr int WGM = 2, WGN = 4;   // wave grid
-    static constexpr int BM = 32 * WM * WGM, BN = 32 * WN * WGN, BK = 128;
-    static constexpr int CH = BK / 16, ROWS = 1024 / BK;   // 8 chunks per LDS row, 8 rows per 1 KB copy
+    static constexpr int BM = 32 * WM * WGM, BN = 32 * WN * WGN, BK = BK_;
+    static_assert(BK == 64 || BK == 128, "one or two k-steps per stage");
+    static constexpr int CH = BK / 16, ROWS = 1024 / BK;   // chunks per LDS row, rows per 1 KB copy
     static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE = A_BYTES + B_BYTES;
     static constexpr int LA = BM / ROWS / WIDE_WAVES, LB = BN / ROWS / WIDE_WAVES;   // copies per wave per stage
     static constexpr int LOADS = LA + LB;
     static_assert(LA * ROWS * WIDE_WAVES == BM && LB * ROWS * WIDE_WAVES == BN, "copies split evenly");
 };
 
-template <int FA, int FB, int WM, int WN, int S>
+template <int FA, int FB, int WM, int WN, int BKW, int S>
 __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *__restrict__ a,
                                                                 const float *__restrict__ sa, uint32_t nsa,
                                                                 const uint8_t *__restrict__ b,
                                                                 const float *__restrict__ sb, uint32_t nsb, uint32_t M,
                                                                 uint32_t N, uint32_t K, uint32_t tiles_m,
                                                                 uint32_t tiles, uint16_t *__restrict__ out) {
-    using T = WideTile<WM, WN>;
+    using T = WideTile<WM, WN, BKW>;
     constexpr int BM = T::BM, BN = T::BN, BK = T::BK, CH = T::CH, ROWS = T::ROWS, KS = BK / FK;
     static_assert(S >= 2, "at least double-buffered");
     static_assert((S - 1) * T::LOADS < 64, "vmcnt range");
@@ -403,71 +413,117 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *
             interleave<WM * WN, 2 * (WM + WN), 0>();
             __builtin_amdgcn_sched_barrier(0);
         } else {
-            mfma_rows(0, WM / 2, fa[CUR], fb[CUR]);
-            __builtin_amdgcn_sched_barrier(0);
+            // This k-step's fragments (the stage's last) are in registers once
+            // the wave's LDS reads are done; after the barrier no wave reads
+            // stage t's slot again, so the copy of stage t + S goes there, and
+            // stage t + 1 (landed: the vmcnt wait) is read during all of this
+            // k-step's MFMAs. The reads come before the copies in program
+            // order: they are needed a k-step earlier, and the compiler keeps
+            // LDS reads and LDS-bound copies in order.
+            wait_lgkm0();
             wait_vmcnt<(S - 2) * T::LOADS>();
             lds_barrier();
             issue(clampi(t + S), (int)(t % S));
             read_frags((int)((t + 1) % S), 0, fa[NXT], fb[NXT]);
-            mfma_rows(WM / 2, WM, fa[CUR], fb[CUR]);
-            interleave<WM / 2 * WN, 2 * (WM + WN), T::LOADS>();
+            mfma_rows(0, WM, fa[CUR], fb[CUR]);
+            __builtin_amdgcn_sched_group_barrier(0x060, T::LOADS, 0);
+            interleave<WM * WN, 2 * (WM + WN), 0>();
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    static_assert(KS == 2, "two k-steps per stage");
     uint32_t t = 0;
-    for (; t + 1 < n; t += 2) {
-        kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
-        kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t);
-        kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t + 1);
-        kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t + 1);
-    }
-    if (t < n) {
-        kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
-        kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t);
+    if constexpr (KS == 2) {
+        for (; t + 1 < n; t += 2) {
+            kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
+            kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t);
+            kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t + 1);
+            kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t + 1);
+        }
+        if (t < n) {
+            kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
+            kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, t);
+        }
+    } else {
+        for (; t + 1 < n; t += 2) {
+            kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
+            kstep(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}, t + 1);
+        }
+        if (t < n) kstep(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, t);
     }
     wait_vmcnt<0>();   // the clamped surplus copies land before LDS is released
 
-    // Epilogue: lane l holds output row m0 + ... + l % 32 and, per group g of
-    // four accumulators, four consecutive columns; one 8-byte store each.
+    // Epilogue through LDS (the operand ring is free once every wave is past
+    // the barrier): lane l holds output row l % 32 of each 32-row tile and,
+    // per group g of four accumulators, four consecutive columns; the scaled
+    // bf16 values go to a row-major BM x BN tile whose 16-byte chunks are
+    // XOR-swizzled by row (chunk c of row r in slot c ^ (r % CC)), then each
+    // wave stores whole tile rows with 16-byte stores, so every store
+    // instruction writes contiguous row segments rather than 16 bytes of each
+    // of 32 rows.
+    constexpr int CC = BN / 8, RB = BN * 2;   // 16-byte chunks / bytes of a bf16 tile row
+    static_assert(S * T::STAGE >= BM * RB, "the output tile fits the operand ring");
+    // Scales as (pointer, stride): no scale reads 1.0 from one_f32, a single
+    // scale has stride 0, so the loads below take no branches.
+    const float *sap = nsa == 0 ? &one_f32 : sa, *sbp = nsb == 0 ? &one_f32 : sb;
+    const uint32_t sas = nsa > 1, sbs = nsb > 1;
+    // The lane index through an empty asm: the epilogue's addresses and scale
+    // loads are computed here rather than hoisted before the main loop.
+    uint32_t te = tid;
+    asm volatile("" : "+v"(te));
+    const uint32_t rle = te & 31, he = (te >> 5) & 1;
+    float sbv[WN][4][4];
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                sbv[j][g][e] = sbp[(n0 + wn * (32 * WN) + j * 32 + 8 * g + 4 * he + e) * sbs];
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
-        const uint32_t m = m0 + wm * (32 * WM) + i * 32 + rl;
-        const float sam = nsa == 0 ? 1.0f : (nsa == 1 ? sa[0] : sa[m]);
-        uint16_t *orow = out + (size_t)m * N;
+        const uint32_t r = wm * (32 * WM) + i * 32 + rle;
+        const float sam = sap[(m0 + r) * sas];
+        uint8_t *lrow = lds + r * RB;
 #pragma unroll
         for (int j = 0; j < WN; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const uint32_t nb = n0 + wn * (32 * WN) + j * 32 + 8 * g + 4 * h;
+                const uint32_t c = wn * (4 * WN) + 4 * j + g;   // columns 8 c .. 8 c + 7 of the tile
                 float o[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float sbn = nsb == 0 ? 1.0f : (nsb == 1 ? sb[0] : sb[nb + e]);
-                    o[e] = acc[i][j][4 * g + e] * sam * sbn;
-                }
+                for (int e = 0; e < 4; ++e) o[e] = acc[i][j][4 * g + e] * sam * sbv[j][g][e];
                 const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
                 const uint32_t hi = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
-                *reinterpret_cast<u32x2 *>(orow + nb) = u32x2{lo, hi};
+                *reinterpret_cast<u32x2 *>(lrow + ((c ^ (r % CC)) * 16) + 8 * he) = u32x2{lo, hi};
             }
+    }
+    __syncthreads();
+    constexpr int RPP = 64 * WIDE_WAVES / CC;   // tile rows per pass of the block
+    static_assert(BM % RPP == 0, "whole passes");
+#pragma unroll
+    for (int p = 0; p < BM / RPP; ++p) {
+        const uint32_t r = p * RPP + te / CC, c = te % CC;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + ((c ^ (r % CC)) * 16));
+        *reinterpret_cast<u32x4 *>(out + (size_t)(m0 + r) * N + n0 + 8 * c) = v;
     }
 }
 
 // Whether the wide (WM, WN) form takes this product: whole tiles, K in whole
-// stages, byte offsets in 31 bits, 8-byte aligned output rows.
-template <int WM, int WN>
+// stages, byte offsets in 31 bits, 16-byte aligned output rows.
+template <int WM, int WN, int BK = 128>
 bool wide_fits(const Fp8Args &g) {
-    using T = WideTile<WM, WN>;
+    using T = WideTile<WM, WN, BK>;
     return g.M % T::BM == 0 && g.N % T::BN == 0 && g.K % T::BK == 0 && (uint64_t)g.M * g.K < (1ull << 31) &&
-           (uint64_t)g.N * g.K < (1ull << 31) && reinterpret_cast<uintptr_t>(g.out) % 8 == 0;
+           (uint64_t)g.N * g.K < (1ull << 31) && reinterpret_cast<uintptr_t>(g.out) % 16 == 0;
 }
 
-template <int WM, int WN, int S>
+template <int WM, int WN, int BK, int S>
 int launch_fp8_wide(const Fp8Args &g, hipStream_t st) {
-    using T = WideTile<WM, WN>;
+    using T = WideTile<WM, WN, BK>;
     const uint32_t tiles_m = g.M / T::BM, tiles = tiles_m * (g.N / T::BN);
 #define RENG_FP8_WIDE(A, B)                                                                                      \
-    hipLaunchKernelGGL((gemm_fp8_wide<A, B, WM, WN, S>), dim3(tiles), dim3(64 * WIDE_WAVES), 0, st, g.a, g.sa, \
+    hipLaunchKernelGGL((gemm_fp8_wide<A, B, WM, WN, BK, S>), dim3(tiles), dim3(64 * WIDE_WAVES), 0, st, g.a, g.sa, \
                        g.nsa, g.b, g.sb, g.nsb, g.M, g.N, g.K, tiles_m, tiles, g.out)
     if (g.fa == RENG_HIP_E4M3 && g.fb == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 0);
     else if (g.fa == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 1);
@@ -494,8 +550,8 @@ int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, con
     // Whole 256 x 256 / 256 x 128 tiles: the 8-wave form, measured 10-17%
     // faster on the M = 1024 prefill shapes than the 4-wave tiles below
     // (256 x 128 with three stages once 256 x 256 tiles no longer fill the CUs).
-    if (t256 >= cus && wide_fits<4, 2>(g)) return launch_fp8_wide<4, 2, 2>(g, st);
-    if (t256 < cus && 2 * t256x128 >= cus && wide_fits<4, 1>(g)) return launch_fp8_wide<4, 1, 3>(g, st);
+    if (t256 >= cus && wide_fits<4, 2>(g)) return launch_fp8_wide<4, 2, 128, 2>(g, st);
+    if (t256 < cus && 2 * t256x128 >= cus && wide_fits<4, 1>(g)) return launch_fp8_wide<4, 1, 128, 3>(g, st);
     if (t256 >= cus) return launch_fp8_cfg<4, 4, 2, 2>(g, st);
     if (t128 >= cus) return K > 8192 ? launch_fp8_cfg<4, 2, 2, 3>(g, st) : launch_fp8_cfg<2, 2, 2, 2>(g, st);
     if (K > 8192 && 2 * t128 >= cus) return launch_fp8_cfg<4, 2, 2, 3>(g, st);

@@ -236,6 +236,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
 
     // Lane l holds output row m = ... + l % 32 and, per group g of four
     // accumulators, the four consecutive columns n = ... + 8 g + 4 h + e.
+    const float *sp = scales ? scales : &one_f32;   // (pointer, stride): no branch per scale
+    const uint32_t ss = scales != nullptr;
     auto store_tile = [&](uint32_t t) __attribute__((always_inline)) {
         const uint32_t m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
 #pragma unroll
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const uint32_t nn = nb + e < N ? nb + e : N - 1;
-                        o[e] = acc[i][j][4 * g + e] * (scales ? scales[nn] : 1.0f);
+                        o[e] = acc[i][j][4 * g + e] * sp[nn * ss];
                     }
                     if (vec_out && nb + 3 < N) {
                         const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
@@ -264,6 +266,61 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
                             if (nb + e < N) orow[nb + e] = (uint16_t)f32_to_bf16_bits(o[e]);
                     }
                 }
+        }
+    };
+    // The block's only tile (without SK), once no copy into the ring is in
+    // flight: the scaled bf16 values go to a row-major BM x BN tile in LDS
+    // (16-byte chunk c of row r in slot c ^ (r % CC)), then the block stores
+    // whole tile rows, 16 bytes per lane, rather than 8 bytes of each of 32
+    // rows per store instruction.
+    auto store_tile_lds = [&](uint32_t t) __attribute__((always_inline)) {
+        constexpr int CC = BN / 8, RB = BN * 2, RPP = 64 * T::W / CC;   // chunks, bytes, rows per pass
+        static_assert(S * T::STAGE >= BM * RB, "the output tile fits the operand ring");
+        static_assert(BM % RPP == 0, "whole passes");
+        const uint32_t m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+        wait_vmcnt<0>();
+        __syncthreads();
+        // The lane index through an empty asm: the epilogue's addresses are
+        // computed here rather than hoisted before the main loop (where they
+        // would hold registers through it).
+        uint32_t te = tid;
+        asm volatile("" : "+v"(te));
+        const uint32_t rle = te & 31, he = (te >> 5) & 1;
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const uint32_t r = wm * (32 * WM) + i * 32 + rle;
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const uint32_t c = wn * (4 * WN) + 4 * j + g;   // columns 8 c .. 8 c + 7 of the tile
+                    const uint32_t nb = n0 + 8 * c + 4 * he;
+                    float o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t nn = nb + e < N ? nb + e : N - 1;
+                        o[e] = acc[i][j][4 * g + e] * sp[nn * ss];
+                    }
+                    const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
+                    const uint32_t hi = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
+                    *reinterpret_cast<u32x2 *>(lds + r * RB + ((c ^ (r % CC)) * 16) + 8 * he) = u32x2{lo, hi};
+                }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < BM / RPP; ++p) {
+            const uint32_t r = p * RPP + te / CC, c = te % CC, m = m0 + r, nc = n0 + 8 * c;
+            if (m >= M || nc >= N) continue;
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + ((c ^ (r % CC)) * 16));
+            uint16_t *dst = y + (size_t)m * N + nc;
+            if (vec_out && nc + 8 <= N) {
+                *reinterpret_cast<u32x4 *>(dst) = v;
+            } else {
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (nc + e < N) dst[e] = (uint16_t)(w[e / 2] >> (16 * (e % 2)));
+            }
         }
     };
     // A partial slot holds BM x BN floats: wave w's WM WN 16 accumulators,
@@ -318,7 +375,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
                 return;
             }
         }
-        store_tile(t);
+        if constexpr (SK) store_tile(t);
+        else store_tile_lds(t);
         zero_acc();
     };
 
@@ -381,7 +439,9 @@ int launch_tiles_cfg(const uint16_t *x, const uint8_t *codes, const float *scale
     using T = Tile<WGM, WGN, WM, WN, BK>;
     const uint32_t tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
     const uint32_t tiles = tiles_m * tiles_n;
-    const uint32_t vec_out = N % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0;
+    // Whole 16-byte chunks of output rows (the LDS-staged store; under SK the
+    // direct store of 8-byte groups, which this implies).
+    const uint32_t vec_out = N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
     if (!SK) grid = tiles;
     hipLaunchKernelGGL((w8a16_tiles<F, WGM, WGN, WM, WN, BK, S, SK>), dim3(grid), dim3(64 * T::W), 0, st, x, codes,
                        scales, M, N, K, tiles_m, tiles, y, vec_out, part, cnt);

@@ -12,6 +12,10 @@ namespace pipe {
 
 constexpr int XCDS = 8;    // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
+// The scale an unscaled operand reads, so that epilogues load a scale through
+// (pointer, stride) without branching on the scale form.
+static __device__ const float one_f32 = 1.0f;
+
 // Slot permutation of an LDS row of CH 16-byte chunks: chunk c of tile row r
 // sits in slot c ^ swz(r). A fragment read takes 32 consecutive rows at one
 // chunk; with these permutations any 8 consecutive rows use 8 distinct slots
@@ -32,6 +36,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt is six bits");
     __builtin_amdgcn_s_waitcnt((N & 0xf) | (7 << 4) | (0xf << 8) | ((N >> 4) << 14));
 }
+
+// s_waitcnt lgkmcnt(0): the wave's LDS reads (and scalar loads) are done.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14)); }
 
 // One global_load_lds_dwordx4: 16 bytes per lane from
 // g into LDS at l + 16 * lane (l is wave-uniform). A __device__ function
