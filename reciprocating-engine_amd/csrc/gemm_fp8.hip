@@ -159,10 +159,8 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma(const uint8_t *__restrict__
     read_frags(0, 0, fa[0], fb[0]);
 
     // One k-step on the fragment set CUR while the next k-step's fragments go
-    // into the other set. The last k-step of a stage splits its MFMAs around
-    // the barrier that publishes stage t + 1. Every fragment of stage t is in
-    // registers by then (the first half's MFMAs waited for them), so after the
-    // barrier the copy of stage t + S goes into stage t's slot.
+    // into the other set; the last k-step of a stage starts with the barrier
+    // that publishes stage t + 1 and frees stage t's slot.
     auto kstep = [&](auto cur_c, auto ks_c, uint32_t t) {
         constexpr int CUR = decltype(cur_c)::value, NXT = CUR ^ 1, KSI = decltype(ks_c)::value;
         if constexpr (KSI + 1 < KS) {
@@ -175,9 +173,10 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma(const uint8_t *__restrict__
             // the wave's LDS reads are done; after the barrier no wave reads
             // stage t's slot again, so the copy of stage t + S goes there, and
             // stage t + 1 (landed: the vmcnt wait) is read during all of this
-            // k-step's MFMAs. The reads come before the copies in program
-            // order: they are needed a k-step earlier, and the compiler keeps
-            // LDS reads and LDS-bound copies in order.
+            // k-step's MFMAs. The copies go out first, back to back: the
+            // compiler keeps LDS reads behind LDS-bound copies issued before
+            // them, and reads placed ahead of the copies in program order get
+            // a vmcnt wait on those copies.
             wait_lgkm0();
             wait_vmcnt<(S - 2) * T::LOADS>();
             lds_barrier();
@@ -321,7 +320,6 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *
     constexpr int BM = T::BM, BN = T::BN, BK = T::BK, CH = T::CH, ROWS = T::ROWS, KS = BK / FK;
     static_assert(S >= 2, "at least double-buffered");
     static_assert((S - 1) * T::LOADS < 64, "vmcnt range");
-    static_assert(WM % 2 == 0, "the last k-step splits the wave's rows in two");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * T::STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -417,9 +415,10 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *
             // the wave's LDS reads are done; after the barrier no wave reads
             // stage t's slot again, so the copy of stage t + S goes there, and
             // stage t + 1 (landed: the vmcnt wait) is read during all of this
-            // k-step's MFMAs. The reads come before the copies in program
-            // order: they are needed a k-step earlier, and the compiler keeps
-            // LDS reads and LDS-bound copies in order.
+            // k-step's MFMAs. The copies go out first, back to back: the
+            // compiler keeps LDS reads behind LDS-bound copies issued before
+            // them, and reads placed ahead of the copies in program order get
+            // a vmcnt wait on those copies.
             wait_lgkm0();
             wait_vmcnt<(S - 2) * T::LOADS>();
             lds_barrier();
