@@ -24,7 +24,13 @@ passes, an IEEE divide per element, <= 8 threads by reng-fp8's split rule)
 timed on this host over layers 0-7 of the same set; those layers are also
 compared bit for bit with the GPU's codes and scales.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--part ...]
+roofline.traffic is the dominant quantize kernel's HBM bytes per launch from two
+rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE) that the default run starts as
+child processes over its own quantize part, scaled by a 1 GiB device copy in
+the same pass (--no-traffic, or no rocprofv3: the committed summary instead;
+roofline.traffic_source says which).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--no-traffic] [--part ...]
 """
 import argparse
 import json
@@ -466,6 +472,62 @@ def decode_cpu_record():
             "the oracle's restatement of layer_cpu with numpy BLAS matrix-vector products (median of 3)"}
 
 
+def measure_traffic(fmt):
+    """HBM bytes per launch of the dominant quantize kernel, measured now: two rocprofv3 --pmc
+    passes (FETCH_SIZE, then WRITE_SIZE, one counter each) over this script's quantize part, run as
+    child processes with the 1 GiB device-copy calibration; each counter is scaled by what it reads
+    for that copy in the same pass. The dominant kernel is the quantize_rows_fast launch form with
+    the most bytes over the pass (rows of 4096 on the Llama-3.1-8B set). Returns (bytes, note);
+    bytes is None when rocprofv3 is missing or a pass gives no usable counters."""
+    import csv
+    import glob
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    tmp = tempfile.mkdtemp(prefix="reng_pmc_", dir="/tmp")
+    per_launch = {}
+    try:
+        for ctr, copy_bytes in (("FETCH_SIZE", 1 << 30), ("WRITE_SIZE", 1 << 30)):
+            out = os.path.join(tmp, ctr)
+            cmd = [exe, "--pmc", ctr, "--output-format", "csv", "-d", out, "-o", "run", "--", sys.executable,
+                   os.path.abspath(__file__), "--part", "quantize", "--steps", "1", "--warmup", "1", "--no-cpu",
+                   "--no-extras", "--format", fmt, "--copy-calibration"]
+            proc = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+                                    stderr=subprocess.DEVNULL, start_new_session=True)
+            try:
+                proc.wait(timeout=240)
+            except subprocess.TimeoutExpired:
+                os.killpg(proc.pid, signal.SIGKILL)
+                proc.wait()
+                return None, f"rocprofv3 --pmc {ctr} timed out"
+            # rocprofv3 may end with a signal after the program finished and its files are whole:
+            # the counter file decides.
+            groups = {}
+            for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
+                with open(path) as f:
+                    for r in csv.DictReader(f):
+                        if r.get("Counter_Name") != ctr:
+                            continue
+                        groups.setdefault((r["Kernel_Name"], r["Grid_Size"]), []).append(float(r["Counter_Value"]))
+            copies = [max(v) for (name, _), v in groups.items() if "copyBuffer" in name]
+            quant = [v for (name, _), v in groups.items() if "quantize_rows_fast" in name]
+            if not copies or not quant or max(copies) <= 0:
+                return None, f"rocprofv3 --pmc {ctr}: no calibration copy or quantize kernel in the counters"
+            scale = copy_bytes / (max(copies) * 1024)
+            dom = max(quant, key=sum)
+            per_launch[ctr] = sum(dom) / len(dom) * 1024 * scale
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return int(per_launch["FETCH_SIZE"] + per_launch["WRITE_SIZE"]), (
+        "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over `bench.py --part quantize` in this run, "
+        "each scaled by the counter's reading for a 1 GiB device copy")
+
+
 def read_traffic(kind):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC
     summary (profiles/<kind>_traffic.txt: `fetch_bytes` and `write_bytes` lines,
@@ -490,6 +552,9 @@ def main():
     ap.add_argument("--format", default="e4m3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes that measure the dominant kernel's HBM "
+                         "traffic (the committed profiles/quantize_traffic.txt is reported instead)")
     ap.add_argument("--part", default="all",
                     choices=["all", "quantize", "gemv", "skinny", "tiles", "prefill", "f32", "decode", "qwen32b",
                              "host"],
@@ -556,9 +621,16 @@ def main():
         f"per config {res['configs']}")
     dom = res["dominant"]
     achieved = dom["bytes_per_launch"] / dom["secs_per_launch"] / 1e9
-    traffic = read_traffic("quantize")
+    traffic, traffic_src = None, None
+    if args.part == "all" and not args.no_traffic:
+        traffic, why = measure_traffic(args.format)
+        traffic_src = why if traffic is not None else None
+        log(f"traffic per launch: {traffic} B ({why})")
+    if traffic is None:
+        traffic = read_traffic("quantize")
+        traffic_src = "profiles/quantize_traffic.txt (committed rocprofv3 summary)" if traffic is not None else None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic,
+                "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "kernel": f"quantize_rows_fast (bf16, {args.format}, rows of {dom['cols']})",
                 "algorithmic_bytes_per_launch": int(dom["bytes_per_launch"]),
                 "mean_launch_us": round(dom["secs_per_launch"] * 1e6, 1)}
