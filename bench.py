@@ -500,7 +500,7 @@ def measure_traffic(fmt):
             proc = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
                                     stderr=subprocess.DEVNULL, start_new_session=True)
             try:
-                proc.wait(timeout=240)
+                proc.wait(timeout=90)   # a pass takes seconds; a stuck one must not hold the bench
             except subprocess.TimeoutExpired:
                 os.killpg(proc.pid, signal.SIGKILL)
                 proc.wait()
