@@ -280,18 +280,53 @@ def bench_w8a16_tiles(torch, R, gen):
 
 
 def bench_fp8_gemm(torch, R, gen, M, N, K):
-    w = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16).view(-1)
-    qw = R.quantize_with(w, N, K, "e4m3", "pcs")
-    del w
+    """fp8 x fp8 at M = 1024 over rotated weight copies, each copy quantized
+    per output channel and the activation per token; beside it hipBLASLt
+    (torch._scaled_mm) on the same codes as the library yardstick, with
+    row-wise scales where this torch takes them, else one scale per tensor."""
+    per = N * K
+    copies = rotation(per)
+    ws = []
+    for _ in range(copies):
+        w = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16).view(-1)
+        ws.append(R.quantize_with(w, N, K, "e4m3", "pcs"))
+        del w
     x = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16).view(-1)
     qa = R.quantize_with(x, M, K, "e4m3", "pcs")     # per-token activation scales
     out = torch.empty(M * N, dtype=torch.bfloat16, device="cuda")
-    secs = graph_time(torch, lambda i: R.gemm_fp8_scaled(qa.codes, "e4m3", qa.scales, qw.codes, "e4m3",
-                                                         qw.scales, M, N, K, out), 10)
+    secs = graph_time(torch, lambda i: R.gemm_fp8_scaled(qa.codes, "e4m3", qa.scales, ws[i % copies].codes, "e4m3",
+                                                         ws[i % copies].scales, M, N, K, out),
+                      max(2 * copies, 10))
     flops = 2 * M * N * K
     ceil = RC.fp8_gemm_ceiling(MI355X, M, N, K)   # fp8 MFMA-bound at M = 1024
-    return {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 1), "TFLOPs": round(flops / secs / 1e12, 1),
-            "mfma_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value}
+    rec = {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 1), "TFLOPs": round(flops / secs / 1e12, 1),
+           "mfma_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value, "rotated_copies": copies}
+    # The same e4m3 codes as OCP float8_e4m3fn (codes 0x00-0x77 mean the same value in both).
+    a8 = qa.codes.view(torch.float8_e4m3fn).view(M, K)
+    b8 = [q.codes.view(torch.float8_e4m3fn).view(N, K).t() for q in ws]   # [K, N], column-major
+    forms = (("rowwise", lambda q: (qa.scales.view(M, 1), q.scales.view(1, N))),
+             ("tensorwise", lambda q: (torch.ones((), device="cuda"), torch.ones((), device="cuda"))))
+    for name, scales in forms:
+        sc = [scales(q) for q in ws]
+        try:
+            torch._scaled_mm(a8, b8[0], sc[0][0], sc[0][1], out_dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+        except (RuntimeError, NotImplementedError) as e:
+            rec.setdefault("hipblaslt_refused", {})[name] = str(e).splitlines()[0][:160]
+            continue
+        hsecs = graph_time(torch, lambda i: torch._scaled_mm(a8, b8[i % copies], sc[i % copies][0],
+                                                             sc[i % copies][1], out_dtype=torch.bfloat16),
+                           max(2 * copies, 10))
+        rec["hipblaslt"] = {"us": round(hsecs * 1e6, 1), "scales": name, "ours_over_hipblaslt": round(secs / hsecs, 3)}
+        if name == "rowwise":
+            # Both products of copy 0 side by side: the library as an
+            # independent check of the whole output at full size.
+            R.gemm_fp8_scaled(qa.codes, "e4m3", qa.scales, ws[0].codes, "e4m3", ws[0].scales, M, N, K, out)
+            ref = torch._scaled_mm(a8, b8[0], sc[0][0], sc[0][1], out_dtype=torch.bfloat16).float()
+            d = out.view(M, N).float() - ref
+            rec["hipblaslt"]["rel_l2"] = float(d.norm() / ref.norm())
+        break
+    return rec
 
 
 def cpu_f32_quantize(x_host, rows, cols):

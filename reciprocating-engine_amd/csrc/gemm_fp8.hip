@@ -291,33 +291,32 @@ int launch_fp8_cfg(const Fp8Args &g, hipStream_t st) {
 // fragment reads or the stage barrier; the 256 x 256 tile halves the operand
 // bytes each output needs against 128 x 128.
 
-constexpr int WIDE_WAVES = 8;
-
 __device__ __forceinline__ void copy16_buf(__amdgpu_buffer_rsrc_t r, uint8_t *l, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)l, 16, voff, soff, 0, 0);
 }
 
-template <int WM, int WN, int BK_ = 128>
+// WGM x WGN waves (default 2 x 4), each owning WM x WN MFMA tiles of 32 x 32.
+template <int WM, int WN, int BK_ = 128, int WGM_ = 2, int WGN_ = 4>
 struct WideTile {
-    static constexpr int WGM = 2, WGN = 4;   // wave grid
+    static constexpr int WGM = WGM_, WGN = WGN_, NW = WGM * WGN;   // wave grid, waves
     static constexpr int BM = 32 * WM * WGM, BN = 32 * WN * WGN, BK = BK_;
     static_assert(BK == 64 || BK == 128, "one or two k-steps per stage");
     static constexpr int CH = BK / 16, ROWS = 1024 / BK;   // chunks per LDS row, rows per 1 KB copy
     static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE = A_BYTES + B_BYTES;
-    static constexpr int LA = BM / ROWS / WIDE_WAVES, LB = BN / ROWS / WIDE_WAVES;   // copies per wave per stage
+    static constexpr int LA = BM / ROWS / NW, LB = BN / ROWS / NW;   // copies per wave per stage
     static constexpr int LOADS = LA + LB;
-    static_assert(LA * ROWS * WIDE_WAVES == BM && LB * ROWS * WIDE_WAVES == BN, "copies split evenly");
+    static_assert(LA * ROWS * NW == BM && LB * ROWS * NW == BN, "copies split evenly");
 };
 
-template <int FA, int FB, int WM, int WN, int BKW, int S>
-__global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *__restrict__ a,
+template <int FA, int FB, int WM, int WN, int BKW, int S, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_fp8_wide(const uint8_t *__restrict__ a,
                                                                 const float *__restrict__ sa, uint32_t nsa,
                                                                 const uint8_t *__restrict__ b,
                                                                 const float *__restrict__ sb, uint32_t nsb, uint32_t M,
                                                                 uint32_t N, uint32_t K, uint32_t tiles_m,
                                                                 uint32_t tiles, uint16_t *__restrict__ out) {
-    using T = WideTile<WM, WN, BKW>;
-    constexpr int BM = T::BM, BN = T::BN, BK = T::BK, CH = T::CH, ROWS = T::ROWS, KS = BK / FK;
+    using T = WideTile<WM, WN, BKW, WGM, WGN>;
+    constexpr int BM = T::BM, BN = T::BN, BK = T::BK, CH = T::CH, ROWS = T::ROWS, KS = BK / FK, NT = 64 * T::NW;
     static_assert(S >= 2, "at least double-buffered");
     static_assert((S - 1) * T::LOADS < 64, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * T::STAGE];
@@ -455,11 +454,15 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *
     // the barrier): lane l holds output row l % 32 of each 32-row tile and,
     // per group g of four accumulators, four consecutive columns; the scaled
     // bf16 values go to a row-major BM x BN tile whose 16-byte chunks are
-    // XOR-swizzled by row (chunk c of row r in slot c ^ (r % CC)), then each
-    // wave stores whole tile rows with 16-byte stores, so every store
-    // instruction writes contiguous row segments rather than 16 bytes of each
-    // of 32 rows.
+    // rotated by row (chunk c of row r in slot slot(r, c): c ^ (r % CC) for a
+    // power-of-two CC, else (c + r) % CC), then the block stores whole tile
+    // rows with 16-byte stores, so every store instruction writes contiguous
+    // row segments rather than 16 bytes of each of 32 rows.
     constexpr int CC = BN / 8, RB = BN * 2;   // 16-byte chunks / bytes of a bf16 tile row
+    auto slot = [](uint32_t r, uint32_t c) -> uint32_t {
+        if constexpr ((CC & (CC - 1)) == 0) return c ^ (r % CC);
+        else return (c + r) % CC;
+    };
     static_assert(S * T::STAGE >= BM * RB, "the output tile fits the operand ring");
     // Scales as (pointer, stride): no scale reads 1.0 from one_f32, a single
     // scale has stride 0, so the loads below take no branches.
@@ -494,35 +497,34 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_fp8_wide(const uint8_t *
                 for (int e = 0; e < 4; ++e) o[e] = acc[i][j][4 * g + e] * sam * sbv[j][g][e];
                 const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
                 const uint32_t hi = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
-                *reinterpret_cast<u32x2 *>(lrow + ((c ^ (r % CC)) * 16) + 8 * he) = u32x2{lo, hi};
+                *reinterpret_cast<u32x2 *>(lrow + slot(r, c) * 16 + 8 * he) = u32x2{lo, hi};
             }
     }
     __syncthreads();
-    constexpr int RPP = 64 * WIDE_WAVES / CC;   // tile rows per pass of the block
-    static_assert(BM % RPP == 0, "whole passes");
+    static_assert((BM * CC) % NT == 0, "whole passes");
 #pragma unroll
-    for (int p = 0; p < BM / RPP; ++p) {
-        const uint32_t r = p * RPP + te / CC, c = te % CC;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + ((c ^ (r % CC)) * 16));
+    for (int p = 0; p < BM * CC / NT; ++p) {
+        const uint32_t i = p * NT + te, r = i / CC, c = i % CC;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + slot(r, c) * 16);
         *reinterpret_cast<u32x4 *>(out + (size_t)(m0 + r) * N + n0 + 8 * c) = v;
     }
 }
 
 // Whether the wide (WM, WN) form takes this product: whole tiles, K in whole
 // stages, byte offsets in 31 bits, 16-byte aligned output rows.
-template <int WM, int WN, int BK = 128>
+template <int WM, int WN, int BK = 128, int WGM = 2, int WGN = 4>
 bool wide_fits(const Fp8Args &g) {
-    using T = WideTile<WM, WN, BK>;
+    using T = WideTile<WM, WN, BK, WGM, WGN>;
     return g.M % T::BM == 0 && g.N % T::BN == 0 && g.K % T::BK == 0 && (uint64_t)g.M * g.K < (1ull << 31) &&
            (uint64_t)g.N * g.K < (1ull << 31) && reinterpret_cast<uintptr_t>(g.out) % 16 == 0;
 }
 
-template <int WM, int WN, int BK, int S>
+template <int WM, int WN, int BK, int S, int WGM = 2, int WGN = 4>
 int launch_fp8_wide(const Fp8Args &g, hipStream_t st) {
-    using T = WideTile<WM, WN, BK>;
+    using T = WideTile<WM, WN, BK, WGM, WGN>;
     const uint32_t tiles_m = g.M / T::BM, tiles = tiles_m * (g.N / T::BN);
 #define RENG_FP8_WIDE(A, B)                                                                                      \
-    hipLaunchKernelGGL((gemm_fp8_wide<A, B, WM, WN, BK, S>), dim3(tiles), dim3(64 * WIDE_WAVES), 0, st, g.a, g.sa, \
+    hipLaunchKernelGGL((gemm_fp8_wide<A, B, WM, WN, BK, S, WGM, WGN>), dim3(tiles), dim3(64 * T::NW), 0, st, g.a, g.sa, \
                        g.nsa, g.b, g.sb, g.nsb, g.M, g.N, g.K, tiles_m, tiles, g.out)
     if (g.fa == RENG_HIP_E4M3 && g.fb == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 0);
     else if (g.fa == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 1);
@@ -539,18 +541,47 @@ int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, con
                     hipStream_t st) {
     using namespace fp8gemm;
     const Fp8Args g{a, fa, sa, nsa, b, fb, sb, nsb, M, N, K, out};
-    // Tile choice by how many tiles each size gives for the chip (measured on
-    // the M = 1024 prefill shapes): the largest tile that still fills every
-    // CU; 256 x 128 for long K; 64 x 64 for small outputs.
     const uint64_t cus = (uint64_t)device_props().cus;
+    // Whole tiles: the wide forms. Each candidate's time is modelled as
+    // rounds x (c0 + c1 x stages), rounds = ceil(tiles / CUs), stages = K / 128,
+    // with (c0, c1) in microseconds fitted to timings of every form on eleven
+    // products (M 256-2048, N 1024-27648, K 4096-27648; shorter K is an
+    // extrapolation). Most timings lie within 10% of the fit, 64 x 64 and
+    // 256 x 128 up to 26% above it when their tiles take a single round. The
+    // cheapest form runs; on those products that is the fastest one measured.
+    struct Cand {
+        bool fits;
+        uint32_t bm, bn;
+        float c0, c1;
+    };
+    const Cand cands[] = {
+        {wide_fits<4, 2>(g), 256, 256, 16.2f, 1.318f},            // 8 waves, 2 slots
+        {wide_fits<2, 2, 128, 4, 2>(g), 256, 128, 12.2f, 0.739f},  // 8 waves, 3 slots
+        {wide_fits<1, 5, 128, 4, 1>(g), 128, 160, 8.6f, 0.658f},   // 4 waves, 3 slots
+        {wide_fits<2, 2, 128, 2, 2>(g), 128, 128, 6.5f, 0.550f},   // 4 waves, 3 slots
+        {wide_fits<1, 1, 128, 2, 2>(g), 64, 64, 1.1f, 0.246f},     // 4 waves, 4 slots
+    };
+    int pick = -1;
+    float best = 0.0f;
+    for (int i = 0; i < 5; ++i) {
+        if (!cands[i].fits) continue;
+        const uint64_t tiles = (uint64_t)(M / cands[i].bm) * (N / cands[i].bn);
+        const float est = (float)((tiles + cus - 1) / cus) * (cands[i].c0 + cands[i].c1 * (float)(K / 128));
+        if (pick < 0 || est < best) pick = i, best = est;
+    }
+    switch (pick) {
+    case 0: return launch_fp8_wide<4, 2, 128, 2>(g, st);
+    case 1: return launch_fp8_wide<2, 2, 128, 3, 4, 2>(g, st);
+    case 2: return launch_fp8_wide<1, 5, 128, 3, 4, 1>(g, st);
+    case 3: return launch_fp8_wide<2, 2, 128, 3, 2, 2>(g, st);
+    case 4: return launch_fp8_wide<1, 1, 128, 4, 2, 2>(g, st);
+    default: break;
+    }
+    // Ragged shapes: by how many tiles each size gives for the chip (measured
+    // on the M = 1024 prefill shapes): the largest tile that still fills every
+    // CU; 256 x 128 for long K; 64 x 64 for small outputs.
     const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
     const uint64_t t128 = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
-    const uint64_t t256x128 = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
-    // Whole 256 x 256 / 256 x 128 tiles: the 8-wave form, measured 10-17%
-    // faster on the M = 1024 prefill shapes than the 4-wave tiles below
-    // (256 x 128 with three stages once 256 x 256 tiles no longer fill the CUs).
-    if (t256 >= cus && wide_fits<4, 2>(g)) return launch_fp8_wide<4, 2, 128, 2>(g, st);
-    if (t256 < cus && 2 * t256x128 >= cus && wide_fits<4, 1>(g)) return launch_fp8_wide<4, 1, 128, 3>(g, st);
     if (t256 >= cus) return launch_fp8_cfg<4, 4, 2, 2>(g, st);
     if (t128 >= cus) return K > 8192 ? launch_fp8_cfg<4, 2, 2, 3>(g, st) : launch_fp8_cfg<2, 2, 2, 2>(g, st);
     if (K > 8192 && 2 * t128 >= cus) return launch_fp8_cfg<4, 2, 2, 3>(g, st);

@@ -339,10 +339,12 @@ def test_fp8_gemm_ragged_tiles(R, M, N, K):
     check_fp8(R, rng, M, N, K, E4M3, E4M3, sample_cols=160)
 
 
-# Whole-tile shapes take the 8-wave form: 256 x 256 tiles when they fill the
-# CUs (1024 x 16384), 256 x 128 otherwise (512 x 16384, 256 x 32768); K of one,
-# two and three 128-code stages, every format pair and scale form.
-@pytest.mark.parametrize("M,N,K", [(1024, 16384, 256), (512, 16384, 384), (256, 32768, 128)])
+# Whole-tile shapes take the wide forms, one shape per tile the launcher's
+# cost model picks: 256 x 256 (1024 x 16384), 256 x 128 (512 x 16384),
+# 128 x 160 (1024 x 5120), 128 x 128 (1024 x 4096) and 64 x 64 (256 x 32768);
+# K of one to eight 128-code stages, every format pair and scale form.
+@pytest.mark.parametrize("M,N,K", [(1024, 16384, 256), (512, 16384, 384), (1024, 5120, 1024), (1024, 4096, 1024),
+                                   (256, 32768, 128)])
 @pytest.mark.parametrize("fa,fb", [(E4M3, E4M3), (E5M2, E5M2), (E4M3, E5M2), (E5M2, E4M3)])
 def test_fp8_gemm_wide_tiles(R, M, N, K, fa, fb):
     rng = np.random.default_rng(M + N + K + 4 * fa + fb)
