@@ -359,6 +359,11 @@ def bench_f32_quantize(torch, R, gen, rows=2048, cols=2048, cpu=False):
     nbytes = quant_bytes(rows, cols, 4)
     rec = {"rows": rows, "cols": cols, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
            "hbm_frac": round(nbytes / secs / HBM_PEAK, 3), "rotated_copies": copies}
+    # One launch that only reads the same 16.8 MB input, rotated the same way:
+    # what a launch of this size costs before any encode or store.
+    sink = torch.empty(R.stream_read_sink_bytes(), dtype=torch.uint8, device="cuda")
+    rsecs = graph_time(torch, lambda i: R.stream_read(mats[i % copies][0], rows * cols * 4, sink), 2 * copies)
+    rec["read_yardstick"] = {"us": round(rsecs * 1e6, 2), "quantize_over_read": round(secs / rsecs, 3)}
     if cpu:
         import numpy as np
 
