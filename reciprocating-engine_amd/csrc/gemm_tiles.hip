@@ -270,13 +270,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
     };
     // The block's only tile (without SK), once no copy into the ring is in
     // flight: the scaled bf16 values go to a row-major BM x BN tile in LDS
-    // (16-byte chunk c of row r in slot c ^ (r % CC)), then the block stores
-    // whole tile rows, 16 bytes per lane, rather than 8 bytes of each of 32
-    // rows per store instruction.
+    // (16-byte chunk c of row r in slot slot(r, c): c ^ (r % CC) for a
+    // power-of-two CC, else (c + r) % CC), then the block stores whole tile
+    // rows, 16 bytes per lane, rather than 8 bytes of each of 32 rows per
+    // store instruction.
     auto store_tile_lds = [&](uint32_t t) __attribute__((always_inline)) {
-        constexpr int CC = BN / 8, RB = BN * 2, RPP = 64 * T::W / CC;   // chunks, bytes, rows per pass
+        constexpr int CC = BN / 8, RB = BN * 2, NT = 64 * T::W;   // chunks, bytes of a tile row; threads
         static_assert(S * T::STAGE >= BM * RB, "the output tile fits the operand ring");
-        static_assert(BM % RPP == 0, "whole passes");
+        static_assert((BM * CC) % NT == 0, "whole passes");
+        auto slot = [](uint32_t r, uint32_t c) -> uint32_t {
+            if constexpr ((CC & (CC - 1)) == 0) return c ^ (r % CC);
+            else return (c + r) % CC;
+        };
         const uint32_t m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
         wait_vmcnt<0>();
         __syncthreads();
@@ -303,15 +308,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
                     }
                     const uint32_t lo = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
                     const uint32_t hi = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
-                    *reinterpret_cast<u32x2 *>(lds + r * RB + ((c ^ (r % CC)) * 16) + 8 * he) = u32x2{lo, hi};
+                    *reinterpret_cast<u32x2 *>(lds + r * RB + slot(r, c) * 16 + 8 * he) = u32x2{lo, hi};
                 }
         }
         __syncthreads();
 #pragma unroll
-        for (int p = 0; p < BM / RPP; ++p) {
-            const uint32_t r = p * RPP + te / CC, c = te % CC, m = m0 + r, nc = n0 + 8 * c;
+        for (int p = 0; p < BM * CC / NT; ++p) {
+            const uint32_t ix = p * NT + te, r = ix / CC, c = ix % CC, m = m0 + r, nc = n0 + 8 * c;
             if (m >= M || nc >= N) continue;
-            const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + ((c ^ (r % CC)) * 16));
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + slot(r, c) * 16);
             uint16_t *dst = y + (size_t)m * N + nc;
             if (vec_out && nc + 8 <= N) {
                 *reinterpret_cast<u32x4 *>(dst) = v;
@@ -458,14 +463,16 @@ inline bool streamk_suits(uint32_t M, uint32_t N, uint32_t K) {
     return K % 128 == 0 && K >= 8192 && 2 * tile_count(M, N, 128, 128) < (uint64_t)device_props().cus;
 }
 
-// Tile choice (measured on MI355X over M = 128-1024 and the Llama-3.1-8B /
-// Qwen2.5-32B shapes): long K over few tiles runs stream-K on 128 x 128 tiles
-// of 128-code stages (M = 256 [4096, 14336]: 92.8 -> 66.5 us); otherwise the
-// largest tile whose count still covers the chip - 256 x 256 (8 waves of
-// 128 x 64) with a tile per CU; 128 x 256 (8 waves of 64 x 64) with half the
-// CUs or more, which beats 128 x 128 at twice the count (M = 1024
-// [5120, 5120]: 72 against 93 us); 128 x 128 (8 waves of 64 x 32, six
-// stages) from three quarters of the CUs; else 64 x 128. Stream-K takes
+// Tile choice. Long K (K >= 8192) over fewer 128 x 128 tiles than half the
+// CUs runs stream-K on 128 x 128 tiles of 128-code stages (M = 256
+// [4096, 14336]: 92.8 -> 66.5 us). Otherwise each form's time is modelled as
+// rounds x (c0 + c1 x K / 64), rounds = ceil(tiles / CUs), with (c0, c1) in
+// microseconds fitted to graph-replayed timings of every form on eleven
+// products (M 128-1024 over the Llama-3.1-8B and Qwen2.5-32B shapes; most
+// within 16% of the fit), and the cheapest form runs; on those products that
+// is the fastest one measured (M = 256 [4096, 4096] 26.6 -> 21.8 us with
+// 64 x 64 tiles, M = 512 [5120, 5120] 64.4 -> 43.2 us with 128 x 128,
+// M = 1024 [5120, 27648] 328 -> 308 us with 128 x 160). Stream-K takes
 // (G + tiles - 1) BM BN floats of partials (6.3 Mi floats at most on 256
 // CUs) and a counter per tile (fewer than 128).
 template <int F>
@@ -485,13 +492,35 @@ int launch_tiles_f(const uint16_t *x, const uint8_t *codes, const float *scales,
         if (rc) return rc;
         return launch_tiles_cfg<F, 2, 4, 2, 1, 128, 3, true>(x, codes, scales, M, N, K, y, st, grid, part, cnt);
     }
-    if (tile_count(M, N, 256, 256) >= cus)
-        return launch_tiles_cfg<F, 2, 4, 4, 2, 64, 3, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
-    if (2 * tile_count(M, N, 128, 256) >= cus)
-        return launch_tiles_cfg<F, 2, 4, 2, 2, 64, 3, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
-    if (4 * t128 >= 3 * cus)
-        return launch_tiles_cfg<F, 2, 4, 2, 1, 64, 6, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
-    return launch_tiles_cfg<F, 2, 4, 1, 1, 64, 6, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
+    struct Cand {
+        uint32_t bm, bn;
+        float c0, c1;
+        bool fits;
+    };
+    const Cand cands[] = {
+        {256, 256, 28.6f, 1.130f, true},            // 8 waves of 128 x 64, 64-code stages, 3 slots
+        {128, 256, 18.1f, 0.703f, true},            // 8 waves of 64 x 64, 3 slots
+        {128, 160, 5.6f, 0.700f, K % 128 == 0},     // 4 waves of 32 x 160, 128-code stages, 2 slots
+        {128, 128, 10.2f, 0.465f, true},            // 8 waves of 64 x 32, 6 slots
+        {64, 128, 5.0f, 0.348f, true},              // 8 waves of 32 x 32, 6 slots
+        {64, 64, 0.0f, 0.251f, true},               // 4 waves of 32 x 32, 6 slots
+    };
+    int pick = 0;
+    float best = 0.0f;
+    for (int i = 0; i < 6; ++i) {
+        if (!cands[i].fits) continue;
+        const uint64_t rounds = (tile_count(M, N, cands[i].bm, cands[i].bn) + cus - 1) / cus;
+        const float est = (float)rounds * (cands[i].c0 + cands[i].c1 * (float)(K / 64));
+        if (i == 0 || est < best) pick = i, best = est;
+    }
+    switch (pick) {
+    case 0: return launch_tiles_cfg<F, 2, 4, 4, 2, 64, 3, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
+    case 1: return launch_tiles_cfg<F, 2, 4, 2, 2, 64, 3, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
+    case 2: return launch_tiles_cfg<F, 4, 1, 1, 5, 128, 2, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
+    case 3: return launch_tiles_cfg<F, 2, 4, 2, 1, 64, 6, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
+    case 4: return launch_tiles_cfg<F, 2, 4, 1, 1, 64, 6, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
+    default: return launch_tiles_cfg<F, 2, 2, 1, 1, 64, 6, false>(x, codes, scales, M, N, K, y, st, 0, nullptr, nullptr);
+    }
 }
 
 }  // namespace tiles

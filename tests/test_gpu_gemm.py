@@ -226,15 +226,18 @@ def test_skinny_every_output_of_a_qwen_7b_gate_up(R, M):
 
 
 @pytest.mark.parametrize("M, N, K, fmt", [
-    (1024, 16384, 128, E4M3),   # 256 x 256 tiles (one per CU)
-    (512, 8192, 192, E5M2),     # 128 x 256 tiles; K % 128 != 0
-    (256, 12288, 256, E4M3),    # 128 x 128 tiles, six stages
-    (200, 4097, 320, E5M2),     # 64 x 128 tiles; ragged M and N (element stores)
+    (1000, 12288, 1024, E4M3),  # 256 x 256 tiles; ragged M
+    (384, 20480, 1024, E5M2),   # 128 x 256 tiles
+    (200, 20480, 768, E4M3),    # 128 x 160 tiles (4 waves, 128-code stages); ragged M
+    (768, 4097, 1536, E5M2),    # 128 x 128 tiles; ragged N (element stores)
+    (200, 4097, 3072, E4M3),    # 64 x 128 tiles; ragged M and N
+    (96, 8192, 64, E5M2),       # 64 x 64 tiles (4 waves); one stage
+    (512, 8192, 192, E4M3),     # 64 x 64 tiles; K % 128 != 0
 ])
 def test_w8a16_tiles_every_output(R, M, N, K, fmt):
     """More than 64 activation rows take the tiled bf16-MFMA kernel; one shape
-    per tile size the launcher picks on a 256-CU MI355X, every output against
-    the oracle and float64."""
+    per tile form the launcher's cost model picks on a 256-CU MI355X, every
+    output against the oracle and float64."""
     rng = np.random.default_rng(M * 7 + N + K)
     check_w8a16(R, rng, M, N, K, fmt)
 
