@@ -17,7 +17,9 @@ oracle); the fused dequant GEMV at batch 1 on the [14336, 4096] and
 [4096, 14336] shapes rotated past the Infinity Cache, next to a plain read of
 the same bytes (the one-launch read yardstick); the skinny GEMM at batch 8 and
 64 on Qwen2.5-7B shapes; the M = 1024 fp8 x fp8 GEMM on Qwen2.5-32B shapes, each
-beside hipBLASLt (torch._scaled_mm) on the same codes; the fp8 decode step.
+beside hipBLASLt (torch._scaled_mm) on the same codes; the fp8 decode step; the
+quantizer's stream yardstick (the same 2 bytes in and 1 byte out per element
+with no arithmetic, reng_hip_stream_narrow) beside the dominant quantize launch.
 
 The CPU baseline is the oracle (a C restatement of reng-fp8's quantizer: two
 passes, an IEEE divide per element, <= 8 threads by reng-fp8's split rule)
@@ -159,6 +161,20 @@ def time_quantize(torch, R, ws, fmt, steps, warmup):
         "configs": {str(c): {"GBps": v["bytes"] / v["secs"] / 1e9, "launches_per_step": v["launches"] // steps}
                     for c, v in by_cfg.items()},
     }
+
+
+def stream_yardstick(torch, R, ws, quant_gbps):
+    """The quantizer's memory stream with no arithmetic (reng_hip_stream_narrow:
+    2 bytes in, 1 byte out per element) over the set's 58.7 M-element
+    matrices (gate, up, down), rotated and replayed from a hipGraph, beside the
+    dominant quantize kernel's rate. Run after the quantize timings: it
+    overwrites those matrices' codes."""
+    big = [m for m in ws.mats if m[2] * m[3] == 14336 * 4096]
+    n = 14336 * 4096
+    secs = graph_time(torch, lambda i: R.stream_narrow(big[i % len(big)][4], n, big[i % len(big)][5]), 2 * len(big))
+    gbps = 3 * n / secs / 1e9
+    return {"matrices": len(big), "us_per_matrix": round(secs * 1e6, 2), "GBps": round(gbps, 1),
+            "hbm_frac": round(gbps * 1e9 / HBM_PEAK, 4), "quantize_over_stream": round(quant_gbps / gbps, 3)}
 
 
 def cpu_baseline_and_parity(torch, O, ws, fmt, layers=8):
@@ -690,6 +706,8 @@ def main():
         r2 = time_quantize(torch, R, ws, other, args.steps, args.warmup)
         extras[f"quantize_{other}_GBps"] = round(r2["gbps"], 1)
         extras[f"quantize_{other}_ms_per_step"] = round(r2["step_s"] * 1e3, 3)
+        extras["quantize_stream_yardstick"] = stream_yardstick(torch, R, ws, achieved)
+        log("stream yardstick:", extras["quantize_stream_yardstick"])
         del ws
         torch.cuda.empty_cache()
         gen = torch.Generator(device="cuda")

@@ -327,6 +327,15 @@ RENG_HIP_API int reng_hip_verify_hw_convert(int format, uint64_t *mismatches,
 RENG_HIP_API size_t reng_hip_stream_read_sink_bytes(void);
 RENG_HIP_API int reng_hip_stream_read(const void *p, size_t bytes, void *sink, void *stream);
 
+/* The stream yardstick the quantizer is measured against: reads `elems` bf16
+ * values at src (16-byte aligned, elems a positive multiple of 8) and writes
+ * the high byte of each to dst (8-byte aligned), i.e. the quantizer's 2 bytes
+ * in and 1 byte out per element with no arithmetic, in the quantizer's
+ * pattern: 8 KB input chunks per wave, grid-strided over 8 waves per CU, the
+ * next chunk requested before this one is stored. No counterpart in the
+ * reference: it exists to measure the memory system. Asynchronous. */
+RENG_HIP_API int reng_hip_stream_narrow(const void *src, size_t elems, void *dst, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

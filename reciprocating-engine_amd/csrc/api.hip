@@ -468,6 +468,15 @@ RENG_HIP_API int reng_hip_stream_read(const void *p, size_t bytes, void *sink, v
     return launch_stream_read(p, bytes, static_cast<uint32_t *>(sink), as_stream(stream));
 }
 
+RENG_HIP_API int reng_hip_stream_narrow(const void *src, size_t elems, void *dst, void *stream) {
+    clear_error();
+    RENG_REQUIRE(src && dst, "null pointer");
+    RENG_REQUIRE(elems >= 8 && elems % 8 == 0, "elems = %zu is not a positive multiple of 8", elems);
+    RENG_REQUIRE((reinterpret_cast<uintptr_t>(src) & 15) == 0, "src must be 16-byte aligned");
+    RENG_REQUIRE((reinterpret_cast<uintptr_t>(dst) & 7) == 0, "dst must be 8-byte aligned");
+    return launch_stream_narrow(src, elems, dst, as_stream(stream));
+}
+
 RENG_HIP_API int reng_hip_gemm_w8a16_noalloc(const uint16_t *x, const uint8_t *codes, const float *scales,
                                              size_t M, size_t N, size_t K, int format, uint16_t *y,
                                              void *stream) {

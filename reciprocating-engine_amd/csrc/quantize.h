@@ -30,5 +30,7 @@ int fast_key(const QMat &m, int dtype);
 int launch_quantize_group(const QBatch &b, int dtype, int format, int scheme, float backoff,
                           int key, hipStream_t st);
 int launch_row_absmax(const QBatch &b, int dtype, float *out, hipStream_t st);
+// The stream yardstick: elems bf16 in, their high bytes out (elems % 8 == 0).
+int launch_stream_narrow(const void *src, uint64_t elems, void *dst, hipStream_t st);
 
 }  // namespace reng

@@ -523,6 +523,57 @@ int launch_quantize_group(const QBatch &b, int dtype, int format, int scheme, fl
     return rc;
 }
 
+// ------------------------------------------------------------------ stream yardstick
+
+// The quantizer's memory stream with no arithmetic: elems bf16 values in (2
+// bytes each), one byte out per value (its high byte). The pattern of the
+// quantizer without its arithmetic, the fastest of those measured for this
+// stream: a wave takes 8 KB chunks of input (lane l: 16-byte vectors
+// 64 j + l, j < 8) grid-strided over 8 waves per CU, requests the next chunk
+// before it stores this one (8-byte non-temporal stores); block 0 takes the
+// vectors past the last whole chunk.
+__device__ __forceinline__ u32x2 high_bytes(const u32x4 &v) {
+    // bytes 1 and 3 of x, y and of z, w: the high bytes of eight bf16 values
+    return u32x2{__builtin_amdgcn_perm(v.y, v.x, 0x07050301u), __builtin_amdgcn_perm(v.w, v.z, 0x07050301u)};
+}
+
+__global__ __launch_bounds__(64) void stream_narrow_kernel(const u32x4 *__restrict__ src, uint64_t vecs,
+                                                           u32x2 *__restrict__ dst) {
+    constexpr int V = 8;
+    constexpr uint64_t C = 64 * V;   // vectors per chunk
+    const uint64_t chunks = vecs / C, G = gridDim.x;
+    const uint32_t l = threadIdx.x;
+    if (blockIdx.x == 0)
+        for (uint64_t i = chunks * C + l; i < vecs; i += 64)
+            __builtin_nontemporal_store(high_bytes(__builtin_nontemporal_load(src + i)), dst + i);
+    uint64_t c = blockIdx.x;
+    if (c >= chunks) return;
+    u32x4 v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = __builtin_nontemporal_load(src + c * C + j * 64 + l);
+    for (; c < chunks; c += G) {
+        const bool more = c + G < chunks;
+        u32x4 n[V];
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < V; ++j) n[j] = __builtin_nontemporal_load(src + (c + G) * C + j * 64 + l);
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) __builtin_nontemporal_store(high_bytes(v[j]), dst + c * C + j * 64 + l);
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < V; ++j) v[j] = n[j];
+        }
+    }
+}
+
+int launch_stream_narrow(const void *src, uint64_t elems, void *dst, hipStream_t st) {
+    const uint32_t blocks = (uint32_t)device_props().cus * 8;   // 8 waves per CU
+    hipLaunchKernelGGL(stream_narrow_kernel, dim3(blocks), dim3(64), 0, st, static_cast<const u32x4 *>(src),
+                       elems / 8, static_cast<u32x2 *>(dst));
+    return check_launch("stream_narrow");
+}
+
 int launch_row_absmax(const QBatch &b, int dtype, float *out, hipStream_t st) {
     return dtype == RENG_HIP_BF16 ? launch_absmax<uint16_t>(b, out, nullptr, st)
                                   : launch_absmax<float>(b, out, nullptr, st);

@@ -76,6 +76,7 @@ SIGNATURES = {
     "reng_hip_add_bf16_f32": (_I, [_P, _P, _SZ, _P, _P]),
     "reng_hip_stream_read_sink_bytes": (_SZ, []),
     "reng_hip_stream_read": (_I, [_P, _SZ, _P, _P]),
+    "reng_hip_stream_narrow": (_I, [_P, _SZ, _P, _P]),
 }
 
 
@@ -530,6 +531,12 @@ def stream_read(buf, nbytes, sink):
     device tensor of at least stream_read_sink_bytes() bytes)."""
     _check(lib().reng_hip_stream_read(_dev(buf, "buf", nbytes), nbytes,
                                       _dev(sink, "sink", lib().reng_hip_stream_read_sink_bytes()), _stream()))
+
+
+def stream_narrow(src, elems, dst):
+    """The stream yardstick: the high byte of each of elems bf16 values of src
+    into dst (device tensors)."""
+    _check(lib().reng_hip_stream_narrow(_dev(src, "src", 2 * elems), elems, _dev(dst, "dst", elems), _stream()))
 
 
 def stream_read_sink_bytes():

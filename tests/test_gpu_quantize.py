@@ -7,7 +7,7 @@ reference's golden fixture; its unit tests' cases; special values (NaN, +-inf,
 zero rows, bf16 subnormals, out-of-range values) inside rows; every bf16
 pattern against thousands of scales; f32 values within a few ulps of every
 fp8 midpoint; generic shapes (cols not a multiple of 8, strided windows);
-batches; full Llama-3.1-8B layer shapes.
+batches; full Llama-3.1-8B layer shapes; the stream yardstick bench.py measures with.
 """
 import numpy as np
 import pytest
@@ -403,3 +403,16 @@ def test_the_staged_host_entry_over_many_chunks(R, dtype):
                 assert np.array_equal(scales.view(np.uint32), ref.scales.view(np.uint32)), (rows, cols, fmt, sc)
                 bad = np.nonzero(codes != ref.codes)[0]
                 assert bad.size == 0, (rows, cols, fmt, sc, bad[:4])
+
+
+def test_the_stream_yardstick_writes_the_high_bytes(R):
+    """reng_hip_stream_narrow (the quantizer's 2:1 memory stream with no
+    arithmetic, a measuring stick for bench.py): the high byte of every bf16
+    value, on a length that exercises the unrolled loop and its remainder."""
+    rng = np.random.default_rng(12)
+    for n in (8, 8 * 1000003):
+        w = rng.integers(0, 1 << 16, n, dtype=np.uint16)
+        out = torch.empty(n, dtype=torch.uint8, device="cuda")
+        R.stream_narrow(dev(w), n, out)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), (w >> 8).astype(np.uint8)), n
