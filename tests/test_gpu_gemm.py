@@ -229,6 +229,7 @@ def test_skinny_every_output_of_a_qwen_7b_gate_up(R, M):
     (1000, 12288, 1024, E4M3),  # 256 x 256 tiles; ragged M
     (384, 20480, 1024, E5M2),   # 128 x 256 tiles
     (200, 20480, 768, E4M3),    # 128 x 160 tiles (4 waves, 128-code stages); ragged M
+    (200, 20001, 768, E5M2),    # 128 x 160 tiles; ragged M and N (element stores)
     (768, 4097, 1536, E5M2),    # 128 x 128 tiles; ragged N (element stores)
     (200, 4097, 3072, E4M3),    # 64 x 128 tiles; ragged M and N
     (96, 8192, 64, E5M2),       # 64 x 64 tiles (4 waves); one stage
