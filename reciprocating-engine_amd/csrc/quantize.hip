@@ -392,15 +392,22 @@ int encode_key(const FastCfg &c) { return c.vpt * 1000 + c.waves * 10 + (c.full 
 
 // Waves per CU for the register-resident kernel: enough rows in flight to keep
 // HBM busy, few enough that the rows being read and written at one time stay
-// close together (measured on MI355X: 8 waves per CU beat full occupancy).
+// close together (measured on MI355X: 8 waves per CU beat full occupancy; 6
+// for one-wave rows of 8 vectors per lane, i.e. 4096 bf16 or 2048 f32 values:
+// rows of 4096 on the Llama-3.1-8B set 5.74-5.75 -> 5.97-5.98 TB/s, while the
+// multi-wave rows of 5120, 14336 and 27648 lose with fewer).
 constexpr int QUANT_WAVES_PER_CU = 8;
 
 template <typename InT, int F, int VPT, int WAVES, bool CLAMP, bool FULL>
 int launch_fast_t(const QBatch &b, int scheme, float full, const float *fs, const uint32_t *fb,
                   hipStream_t st) {
     auto kern = quantize_rows_fast<InT, F, VPT, WAVES, CLAMP, FULL>;
-    uint64_t grid = (uint64_t)device_props().cus * ((QUANT_WAVES_PER_CU + WAVES - 1) / WAVES);
-    if (grid > b.total_rows) grid = b.total_rows;
+    const uint64_t cus = (uint64_t)device_props().cus;
+    constexpr int WPC = WAVES == 1 && VPT == 8 ? 6 : QUANT_WAVES_PER_CU;
+    uint64_t grid = cus * ((WPC + WAVES - 1) / WAVES);
+    // A launch of at most 8 waves' worth of rows per CU (the f32 [2048, 2048]
+    // matrix) is latency-bound: every row in flight at once.
+    if (b.total_rows <= cus * ((QUANT_WAVES_PER_CU + WAVES - 1) / WAVES) || grid > b.total_rows) grid = b.total_rows;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * WAVES), 0, st, b, scheme, full, fs, fb);
     return check_launch("quantize_rows_fast");
 }
