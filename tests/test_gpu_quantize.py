@@ -298,7 +298,7 @@ def test_one_llama_8b_layer_at_full_size(R, fmt):
 
 def test_qwen_32b_mlp_matrices_at_full_size(R):
     """The C5 set's two row widths at full size: one [27648, 5120] gate/up and
-    one [5120, 27648] down matrix (rows of 27648 take the 6-wave kernel), the
+    one [5120, 27648] down matrix (rows of 27648 take the 9-wave kernel), the
     down one with the bench's injections, bit for bit against the oracle."""
     rng = np.random.default_rng(2025)
     up = bf16_bits((rng.standard_normal((27648, 5120)) * 0.02).astype(np.float32))
