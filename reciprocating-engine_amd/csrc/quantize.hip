@@ -397,16 +397,23 @@ int encode_key(const FastCfg &c) { return c.vpt * 1000 + c.waves * 10 + (c.full 
 // HBM busy, few enough that the rows being read and written at one time stay
 // close together (measured on MI355X: 8 waves per CU beat full occupancy; 6
 // for one-wave rows of 8 vectors per lane, i.e. 4096 bf16 or 2048 f32 values:
-// rows of 4096 on the Llama-3.1-8B set 5.74-5.75 -> 5.97-5.98 TB/s, while the
-// multi-wave rows of 5120, 14336 and 27648 lose with fewer).
+// rows of 4096 on the Llama-3.1-8B set 5.74-5.75 -> 5.97-5.98 TB/s; 10 for
+// two-wave rows of 5 vectors, i.e. 5120 bf16: 5.43-5.59 -> 5.79 TB/s on the
+// Qwen2.5-32B shapes).
 constexpr int QUANT_WAVES_PER_CU = 8;
+template <int VPT, int WAVES>
+constexpr int quant_waves_per_cu() {
+    if constexpr (WAVES == 1 && VPT == 8) return 6;
+    else if constexpr (WAVES == 2 && VPT == 5) return 10;
+    else return QUANT_WAVES_PER_CU;
+}
 
 template <typename InT, int F, int VPT, int WAVES, bool CLAMP, bool FULL>
 int launch_fast_t(const QBatch &b, int scheme, float full, const float *fs, const uint32_t *fb,
                   hipStream_t st) {
     auto kern = quantize_rows_fast<InT, F, VPT, WAVES, CLAMP, FULL>;
     const uint64_t cus = (uint64_t)device_props().cus;
-    constexpr int WPC = WAVES == 1 && VPT == 8 ? 6 : QUANT_WAVES_PER_CU;
+    constexpr int WPC = quant_waves_per_cu<VPT, WAVES>();
     uint64_t grid = cus * ((WPC + WAVES - 1) / WAVES);
     // A launch of at most 8 waves' worth of rows per CU (the f32 [2048, 2048]
     // matrix) is latency-bound: every row in flight at once.
