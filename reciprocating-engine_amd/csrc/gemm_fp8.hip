@@ -519,6 +519,20 @@ bool wide_fits(const Fp8Args &g) {
            (uint64_t)g.N * g.K < (1ull << 31) && reinterpret_cast<uintptr_t>(g.out) % 16 == 0;
 }
 
+// A wide form as a dispatch candidate: whether it takes the product, its
+// tile, and its fitted time model (c0, c1).
+struct WideCand {
+    bool fits;
+    uint32_t bm, bn;
+    float c0, c1;
+};
+
+template <int WM, int WN, int WGM, int WGN>
+WideCand wide_cand(const Fp8Args &g, float c0, float c1) {
+    using T = WideTile<WM, WN, 128, WGM, WGN>;
+    return WideCand{wide_fits<WM, WN, 128, WGM, WGN>(g), (uint32_t)T::BM, (uint32_t)T::BN, c0, c1};
+}
+
 template <int WM, int WN, int BK, int S, int WGM = 2, int WGN = 4>
 int launch_fp8_wide(const Fp8Args &g, hipStream_t st) {
     using T = WideTile<WM, WN, BK, WGM, WGN>;
@@ -549,21 +563,16 @@ int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, con
     // extrapolation). Most timings lie within 10% of the fit, 64 x 64 and
     // 256 x 128 up to 26% above it when their tiles take a single round. The
     // cheapest form runs; on those products that is the fastest one measured.
-    struct Cand {
-        bool fits;
-        uint32_t bm, bn;
-        float c0, c1;
-    };
-    const Cand cands[] = {
-        {wide_fits<4, 2>(g), 256, 256, 16.2f, 1.318f},            // 8 waves, 2 slots
-        {wide_fits<2, 2, 128, 4, 2>(g), 256, 128, 12.2f, 0.739f},  // 8 waves, 3 slots
-        {wide_fits<1, 5, 128, 4, 1>(g), 128, 160, 8.6f, 0.658f},   // 4 waves, 3 slots
-        {wide_fits<2, 2, 128, 2, 2>(g), 128, 128, 6.5f, 0.550f},   // 4 waves, 3 slots
-        {wide_fits<1, 1, 128, 2, 2>(g), 64, 64, 1.1f, 0.246f},     // 4 waves, 4 slots
+    const WideCand cands[] = {
+        wide_cand<4, 2, 2, 4>(g, 16.2f, 1.318f),   // 256 x 256, 8 waves, 2 slots
+        wide_cand<2, 2, 4, 2>(g, 12.2f, 0.739f),   // 256 x 128, 8 waves, 3 slots
+        wide_cand<1, 5, 4, 1>(g, 8.6f, 0.658f),    // 128 x 160, 4 waves, 3 slots
+        wide_cand<2, 2, 2, 2>(g, 6.5f, 0.550f),    // 128 x 128, 4 waves, 3 slots
+        wide_cand<1, 1, 2, 2>(g, 1.1f, 0.246f),    // 64 x 64, 4 waves, 4 slots
     };
     int pick = -1;
     float best = 0.0f;
-    for (int i = 0; i < 5; ++i) {
+    for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
         if (!cands[i].fits) continue;
         const uint64_t tiles = (uint64_t)(M / cands[i].bm) * (N / cands[i].bn);
         const float est = (float)((tiles + cus - 1) / cus) * (cands[i].c0 + cands[i].c1 * (float)(K / 128));
