@@ -509,7 +509,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split16(
 }
 
 // out_h = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s): the
-// splits of attention_split merged. One 256-thread workgroup per head.
+// splits of attention_split merged. One 256-thread workgroup per head. Thread
+// t requests split t's (m, l) and dimension t of every split's o together,
+// before the first barrier, so the merge costs one memory round trip (the o
+// values do not depend on the weights); dimensions past 256 are read after.
 constexpr int COMBINE_THREADS = 256;
 __global__ __launch_bounds__(COMBINE_THREADS) void attention_combine(const float *__restrict__ part, uint32_t nh,
                                                                      uint32_t hd, uint32_t splits,
@@ -519,12 +522,25 @@ __global__ __launch_bounds__(COMBINE_THREADS) void attention_combine(const float
     const uint32_t h = blockIdx.x, tid = threadIdx.x;
     const float *ml = part + (size_t)splits * nh * hd;
     const float m = tid < splits ? ml[((size_t)tid * nh + h) * 2] : -INFINITY;
+    const float l = tid < splits ? ml[((size_t)tid * nh + h) * 2 + 1] : 0.0f;
+    const bool first = tid < hd;
+    float pv[ATT_SPLIT_MAX];
+#pragma unroll
+    for (int i = 0; i < ATT_SPLIT_MAX; ++i)
+        pv[i] = first && (uint32_t)i < splits ? part[((size_t)i * nh + h) * hd + tid] : 0.0f;
     const float mx = block_max(m, red);
     const float w = tid < splits ? expf(m - mx) : 0.0f;
-    const float den = block_sum(tid < splits ? w * ml[((size_t)tid * nh + h) * 2 + 1] : 0.0f, red);
+    const float den = block_sum(tid < splits ? w * l : 0.0f, red);
     if (tid < splits) wsp[tid] = w / den;
     __syncthreads();
-    for (uint32_t d = tid; d < hd; d += COMBINE_THREADS) {
+    if (first) {
+        float v = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ATT_SPLIT_MAX; ++i)
+            if ((uint32_t)i < splits) v += wsp[i] * pv[i];
+        out[(size_t)h * hd + tid] = f32_bf16(v);
+    }
+    for (uint32_t d = tid + COMBINE_THREADS; d < hd; d += COMBINE_THREADS) {
         float v = 0.0f;
 #pragma unroll 16
         for (uint32_t i = 0; i < splits; ++i) v += wsp[i] * part[((size_t)i * nh + h) * hd + d];
