@@ -522,20 +522,28 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
 
 // y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the splits added in order; four
 // consecutive n per thread when N % 4 == 0 (16-byte reads, 8-byte stores).
-// The split loads are issued eight at a time (independent) and added in order.
+// The loads of the first 16 splits are issued together (one memory round
+// trip for the split counts the launcher makes at these shapes), later ones
+// eight at a time; the splits are added in order.
 __device__ __forceinline__ f32x4 sum_splits4(const float *part, uint32_t splits, uint64_t total, uint64_t i) {
     const f32x4 *p = reinterpret_cast<const f32x4 *>(part) + i;
     const uint64_t stride = total / 4;
-    f32x4 a = p[0];
-    uint32_t k = 1;
-    for (; k + 8 <= splits; k += 8) {
-        f32x4 v[8];
+    constexpr uint32_t B = 16;
+    f32x4 v[B];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[(k + u) * stride];
+    for (uint32_t u = 0; u < B; ++u) v[u] = u < splits ? p[u * stride] : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 a = v[0];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) a += v[u];
+    for (uint32_t u = 1; u < B; ++u)
+        if (u < splits) a += v[u];
+    for (uint32_t k = B; k < splits; k += 8) {
+        f32x4 w[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) w[u] = k + u < splits ? p[(k + u) * stride] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+            if (k + u < splits) a += w[u];
     }
-    for (; k < splits; ++k) a += p[k * stride];
     return a;
 }
 
