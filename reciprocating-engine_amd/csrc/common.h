@@ -255,6 +255,20 @@ __device__ __forceinline__ void rope_rotate(float x0, float x1, float c0, float 
 // formed; otherwise h = x. Every thread gets the result. red: 16 floats of LDS.
 constexpr int NORM_VT = 1024;
 
+// A float4's share of the sum of squares, added the way row_inv_rms adds it.
+__device__ __forceinline__ float sum_sq4(float ss, const float4 &v) {
+    return ss + (v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+}
+
+// The end of row_inv_rms: the 16 wave sums in red added in order.
+__device__ __forceinline__ float inv_rms_from(const float *red, uint32_t cols, float eps) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NORM_VT / 64; ++w) s += red[w];
+    const float ms = s / (float)cols;
+    return 1.0f / sqrtf(ms + eps);
+}
+
 template <bool VEC, bool ADD, int NV>
 __device__ __forceinline__ float row_inv_rms(const float *__restrict__ xr, const uint16_t *__restrict__ dr,
                                              float *__restrict__ hr, uint32_t cols, float eps, float *red) {
@@ -275,7 +289,7 @@ __device__ __forceinline__ float row_inv_rms(const float *__restrict__ xr, const
                     v.w += __uint_as_float(w1 & 0xffff0000u);
                     *reinterpret_cast<float4 *>(hr + c) = v;
                 }
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                ss = sum_sq4(ss, v);
             }
         } else {
             for (uint32_t c = vt; c < cols; c += NORM_VT) {
@@ -291,11 +305,7 @@ __device__ __forceinline__ float row_inv_rms(const float *__restrict__ xr, const
         if (lane == 0) red[vt >> 6] = ss;
     }
     __syncthreads();
-    float s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NORM_VT / 64; ++w) s += red[w];
-    const float ms = s / (float)cols;
-    return 1.0f / sqrtf(ms + eps);
+    return inv_rms_from(red, cols, eps);
 }
 
 // bf16 bits (RNE, NaN -> 0x7fc0) of an f32 (lib.rs:41-48).

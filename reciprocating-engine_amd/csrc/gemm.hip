@@ -62,6 +62,16 @@ __device__ __forceinline__ float bf_hi(uint32_t d) { return __uint_as_float(d & 
 
 // ------------------------------------------------------------------ GEMV
 
+// A workgroup barrier that waits for this wave's LDS accesses only (no
+// vmcnt(0) as __syncthreads' fence has), so global loads stay in flight
+// across it; the memory clobbers keep LDS accesses on their side of it.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // v_dot2_f32_bf16: acc + a.lo * b.lo + a.hi * b.hi, f32 accumulation.
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
@@ -188,26 +198,87 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
         const uint32_t rr = row_at(first + lane);
         sv = scales[rr < N ? rr : N - 1];
     };
-    if (r < N) {
+    // The four-column RMSNorm prologue on rows of up to 8192 columns holds its
+    // share of h and gamma in registers (columns 4 tid + 2048 m, m < 4). In
+    // issue order: the scales, h and gamma, then the wave's first two code
+    // groups, every load unconditional (indices clamped; a wave past the last
+    // row reads row N - 1 and stores nothing). Loads leave the vmcnt count in
+    // order, so the prologue waits for h and gamma alone, its barriers wait on
+    // LDS only, and the codes stay in flight through it.
+    constexpr bool REGP = PRO == PRO_NORM_VEC;
+    const bool regp = REGP && K <= 4 * 2048;
+    float4 hreg[4], greg[4];
+    u32x4 q2[CPL];
+    uint32_t r2 = r, g2 = gi + 1;
+    if (g2 == gpr) {
+        g2 = 0;
+        r2 = PAIRS ? ((r & 1) ? r - 1 + 2 * waves : r + 1) : r + waves;
+    }
+    bool second = false;
+    if (regp) {
+        if (scales) scales_from(0);
+        const float *xf = reinterpret_cast<const float *>(x);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t c = tid * 4 + 2048 * m < K ? tid * 4 + 2048 * m : K - 4;
+            hreg[m] = *reinterpret_cast<const float4 *>(xf + c);
+            greg[m] = *reinterpret_cast<const float4 *>(gamma + c);
+        }
+        load(r, gi, qn);
+        // A wave with a single group asks for it again (an L2 hit), not for
+        // another row's bytes.
+        second = r2 < N;
+        load(second ? r2 : r, second ? g2 : gi, q2);
+    } else if (r < N) {
         load(r, gi, qn);
         if (scales) scales_from(0);
     }
-    if constexpr (PRO != PRO_NONE) {
-        const float *xf = reinterpret_cast<const float *>(x);
-        const float inv = row_inv_rms<PRO == PRO_NORM_VEC, false, NORM_VT / 512>(xf, nullptr, nullptr, K, eps, red);
-        uint16_t *dst = reinterpret_cast<uint16_t *>(xs);
-        if constexpr (PRO == PRO_NORM_VEC) {
-            for (uint32_t c = tid * 4; c < K; c += 512 * 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(xf + c);
-                const float4 gv = *reinterpret_cast<const float4 *>(gamma + c);
-                const uint32_t lo = f32_to_bf16_bits(v.x * inv * gv.x) | (f32_to_bf16_bits(v.y * inv * gv.y) << 16);
-                const uint32_t hi = f32_to_bf16_bits(v.z * inv * gv.z) | (f32_to_bf16_bits(v.w * inv * gv.w) << 16);
+    if constexpr (REGP) {
+        if (regp) {
+            // row_inv_rms's sum: virtual thread vt = tid + 512 i takes columns
+            // 4 vt + 4096 u, i.e. m = i + 2 u.
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    if (tid * 4 + 2048 * (i + 2 * u) < K) ss = sum_sq4(ss, hreg[i + 2 * u]);
+                ss = wave_sum_dpp(ss);
+                if (lane == 0) red[(tid + 512 * i) >> 6] = ss;
+            }
+            lds_sync();
+            const float inv = inv_rms_from(red, K, eps);
+            uint16_t *dst = reinterpret_cast<uint16_t *>(xs);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t c = tid * 4 + 2048 * m;
+                if (c >= K) continue;
+                const float4 v = hreg[m], g = greg[m];
+                const uint32_t lo = f32_to_bf16_bits(v.x * inv * g.x) | (f32_to_bf16_bits(v.y * inv * g.y) << 16);
+                const uint32_t hi = f32_to_bf16_bits(v.z * inv * g.z) | (f32_to_bf16_bits(v.w * inv * g.w) << 16);
                 *reinterpret_cast<u32x2 *>(dst + c) = u32x2{lo, hi};
             }
-        } else {
-            for (uint32_t c = tid; c < K; c += 512) dst[c] = (uint16_t)f32_to_bf16_bits(xf[c] * inv * gamma[c]);
+            lds_sync();
         }
-        __syncthreads();
+    }
+    if constexpr (PRO != PRO_NONE) {
+        if (!regp) {
+            const float *xf = reinterpret_cast<const float *>(x);
+            const float inv = row_inv_rms<PRO == PRO_NORM_VEC, false, NORM_VT / 512>(xf, nullptr, nullptr, K, eps, red);
+            uint16_t *dst = reinterpret_cast<uint16_t *>(xs);
+            if constexpr (PRO == PRO_NORM_VEC) {
+                for (uint32_t c = tid * 4; c < K; c += 512 * 4) {
+                    const float4 v = *reinterpret_cast<const float4 *>(xf + c);
+                    const float4 gv = *reinterpret_cast<const float4 *>(gamma + c);
+                    const uint32_t lo = f32_to_bf16_bits(v.x * inv * gv.x) | (f32_to_bf16_bits(v.y * inv * gv.y) << 16);
+                    const uint32_t hi = f32_to_bf16_bits(v.z * inv * gv.z) | (f32_to_bf16_bits(v.w * inv * gv.w) << 16);
+                    *reinterpret_cast<u32x2 *>(dst + c) = u32x2{lo, hi};
+                }
+            } else {
+                for (uint32_t c = tid; c < K; c += 512) dst[c] = (uint16_t)f32_to_bf16_bits(xf[c] * inv * gamma[c]);
+            }
+            __syncthreads();
+        }
     } else if constexpr (XLDS) {
         const u32x4 *src = reinterpret_cast<const u32x4 *>(x);
         u32x4 *dst = reinterpret_cast<u32x4 *>(xs);
@@ -229,7 +300,13 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
             gn = 0;
             rn = PAIRS ? ((r & 1) ? r - 1 + 2 * waves : r + 1) : r + waves;
         }
-        if (rn < N) load(rn, gn, qn);   // none past the wave's last row
+        if (second) {   // (rn, gn) is (r2, g2), requested before the prologue
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) qn[u] = q2[u];
+            second = false;
+        } else if (rn < N) {
+            load(rn, gn, qn);   // none past the wave's last row
+        }
 
         const uint32_t c0 = gi * 64 * CPL + lane;
 #pragma unroll
