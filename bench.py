@@ -177,35 +177,54 @@ def stream_yardstick(torch, R, ws, quant_gbps):
             "hbm_frac": round(gbps * 1e9 / HBM_PEAK, 4), "quantize_over_stream": round(quant_gbps / gbps, 3)}
 
 
+def time_oracle_sample(O, host, fmt, runs=3):
+    """The oracle's quantize_with over host [(rows, cols, bf16 bits)] matrix by matrix,
+    `runs` times; returns (the first run's results, every run's seconds)."""
+    times, refs = [], None
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        out = [O.quantize_with(w, r, c, fmt, "pcs", 1.0, thread_cap=8) for r, c, w in host]
+        times.append(time.perf_counter() - t0)
+        refs = refs or out
+    return refs, times
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def cpu_record(O, host, secs, what):
+    """cpu_baseline record: GB/s of algorithmic bytes at the median of the timed runs."""
+    elems = sum(r * c for r, c, _ in host)
+    nbytes = sum(quant_bytes(r, c) for r, c, _ in host)
+    med = sorted(secs)[len(secs) // 2]
+    threads = max(O.split(r, c) for r, c, _ in host)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "runs_s": [round(t, 2) for t in secs],
+            "sample": (f"{what} ({len(host)} matrices, {elems} elements), the median of {len(secs)} runs "
+                       f"({med:.1f} s), the oracle's C restatement of reng-fp8 quantize_with run matrix by "
+                       f"matrix with reng-fp8's split rule (<= 8 threads), {cpu_model()}, nproc {os.cpu_count()}")}
+
+
 def cpu_baseline_and_parity(torch, O, ws, fmt, layers=8):
     import numpy as np
 
     sample = [m for m in ws.mats if m[0] < layers]
     host = [(m[2], m[3], m[4].cpu().numpy().view(np.uint16)) for m in sample]
-    elems = sum(r * c for r, c, _ in host)
-    nbytes = sum(quant_bytes(r, c) for r, c, _ in host)
-    t0 = time.perf_counter()
-    refs = [O.quantize_with(w, r, c, fmt, "pcs", 1.0, thread_cap=8) for r, c, w in host]
-    secs = time.perf_counter() - t0
+    refs, secs = time_oracle_sample(O, host, fmt)
     mismatched = 0
     for m, ref in zip(sample, refs):
         if not (np.array_equal(m[5].cpu().numpy(), ref.codes)
                 and np.array_equal(m[6].cpu().numpy().view(np.uint32), ref.scales.view(np.uint32))
                 and int(m[7].item()) == ref.exp_bias):
             mismatched += 1
-    model = "unknown CPU"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    threads = max(O.split(r, c) for r, c, _ in host)
-    return ({"value": round(nbytes / secs / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-             "sample": (f"layers 0-{layers - 1} of the same set ({len(sample)} matrices, {elems} elements, "
-                        f"{secs:.1f} s), the oracle's C restatement of reng-fp8 quantize_with run matrix by "
-                        f"matrix with reng-fp8's split rule (<= 8 threads), {model}, nproc {os.cpu_count()}")},
+    return (cpu_record(O, host, secs, f"layers 0-{layers - 1} of the same set"),
             {"matrices": len(sample), "mismatched": mismatched})
 
 
@@ -423,12 +442,15 @@ def bench_qwen32b_quantize(torch, R, fmt="e4m3", steps=3, warmup=1, parity=True)
     if parity:
         import oracle as O
 
+        layer0 = [m for m in wq.mats if m[0] == 0]
+        host = [(m[2], m[3], m[4].cpu().numpy().view(np.uint16)) for m in layer0]
+        refs, secs = time_oracle_sample(O, host, fmt)
         bad = 0
-        for m in [m for m in wq.mats if m[0] == 0]:
-            ref = O.quantize_with(m[4].cpu().numpy().view(np.uint16), m[2], m[3], fmt, "pcs", 1.0)
+        for m, ref in zip(layer0, refs):
             bad += int(not (np.array_equal(m[5].cpu().numpy(), ref.codes)
                             and np.array_equal(m[6].cpu().numpy().view(np.uint32), ref.scales.view(np.uint32))))
         rec["parity"] = {"matrices": 7, "mismatched": bad, "sample": "layer 0 (q, k, v, o, gate, up, down)"}
+        rec["cpu_baseline"] = cpu_record(O, host, secs, "layer 0 of the same set (q, k, v, o, gate, up, down)")
     del wq
     torch.cuda.empty_cache()
     return rec

@@ -1,11 +1,13 @@
 // gemm.hip - consumers of the quantizer's codes on CDNA4 (gfx950).
 //
-// 1. gemv_w8a16     (M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
+// 1. gemv_rows      (M = 1, 1024 < K <= 16384) and gemv_w8a16 (the other
+//                    M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
 //                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]); with
-//                    M = 1 also residual-add, SwiGLU-pair and RoPE-pair
-//                    epilogues and an RMSNorm prologue.
-//    Streams the codes once with 16-byte loads, decodes in registers
-//    (v_cvt_pk_f32_fp8 / _bf8), f32 FMA, one wave per output row.
+//                    M = 1 gemv_w8a16 also has residual-add, SwiGLU-pair and
+//                    RoPE-pair epilogues and an RMSNorm prologue.
+//    Both stream the codes once with 16-byte loads, decode in registers to
+//    bf16 (v_cvt_scalef32_pk_bf16_fp8 / _bf8) and accumulate with
+//    v_dot2_f32_bf16, one wave per output row, in the same order.
 // 2. The other M <= 64: the same product on bf16 MFMA with the codes and the
 //    activation staged through LDS (skinny.hip); larger M in tiles of 64.
 // (The fp8 x fp8 product of gemm_fp8_scaled is in gemm_fp8.hip.)
@@ -66,6 +68,7 @@ __device__ __forceinline__ float bf_hi(uint32_t d) { return __uint_as_float(d & 
 // vmcnt(0) as __syncthreads' fence has), so global loads stay in flight
 // across it; the memory clobbers keep LDS accesses on their side of it.
 __device__ __forceinline__ void lds_sync() {
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -377,196 +380,88 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 
 // ------------------------------------------------------------------ GEMV, M = 1
 
-// One wave streams R consecutive rows of the codes (R K contiguous bytes) in
-// steps of U 1 KB chunks, the next step requested before the current one is
-// consumed, every wave resident from the start. Measured on MI355X against the
-// row-strided walk of gemv_w8a16 (whose waves read one row here, one row
-// 14 MB away there): [14336, 4096] 10.95 -> 10.2-10.5 us, [4096, 14336]
-// 11.6 -> 10.3 us, with a plain 1 KB-chunk read of the same bytes at 9.6-9.8 us.
-//
-// The activation is copied into LDS by global_load_lds before the first codes
-// are requested, and the wave waits only for those copies (vmcnt(U): the U
-// code loads issued after them may still be in flight) before the barrier.
+// One wave per output row, every 1 KB chunk of the row (CPR of them, K <=
+// 16384) requested at the start. In issue order: the row's scale, this
+// thread's share of the activation (into registers, then LDS), the row's
+// codes; the activation is written to LDS and the block barrier waits on LDS
+// only, so the codes stay in flight through it. Every load is an ordinary
+// (compiler-tracked) load, issued unconditionally (indices clamped), so the
+// compiler waits for chunk c alone before consuming it while the later chunks
+// are still in flight. Measured on MI355X against the former walk (R rows per
+// wave in U-chunk steps, untracked loads): [14336, 4096] 10.64 -> 10.12 us,
+// [4096, 4096] 4.92 -> 4.46 us, [4096, 14336] 10.9 us both, with a plain
+// one-launch read of the same codes at 9.5-9.6 us.
 //
 // A lane takes the same 16 codes of every 1 KB chunk (k = 1024 c + 16 lane ..
 // + 16) and adds the products in gemv_w8a16's order (chunks in order, even and
 // odd words into two accumulators, then wave_sum_dpp), so the two kernels give
 // the same bits and the fused forms of gemv_w8a16 equal this GEMV followed by
 // their epilogue. A ragged last chunk (K % 1024 != 0) masks the lanes past K.
-__device__ __forceinline__ void dma16(const void *g, void *l) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void gemv_wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-    __builtin_amdgcn_s_waitcnt((N & 0xf) | (7 << 4) | (0xf << 8) | ((N >> 4) << 14));
-}
-
-// Loads the compiler does not track: it inserts no wait for them (and so
-// none that would also wait for the next step's loads); the kernel waits with
-// gemv_wait_vmcnt and ties each result to that wait with gemv_after_wait. The
-// codes are addressed as a wave-uniform base (SGPRs) plus a 32-bit lane offset.
-__device__ __forceinline__ u32x4 gemv_load16(const uint8_t *base, uint32_t off) {
-    u32x4 v;
-    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(v) : "v"(off), "s"(base) : "memory");
-    return v;
-}
-__device__ __forceinline__ float gemv_load4(const void *p) {
-    float v;
-    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-    return v;
-}
-template <int U>
-__device__ __forceinline__ void gemv_after_wait(u32x4 (&q)[U]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) asm volatile("" : "+v"(q[u]));
-}
-// s_waitcnt vmcnt(n) for a run-time n <= 7.
-__device__ __forceinline__ void gemv_wait_upto(uint32_t n) {
-    switch (n) {
-        case 0: gemv_wait_vmcnt<0>(); break;
-        case 1: gemv_wait_vmcnt<1>(); break;
-        case 2: gemv_wait_vmcnt<2>(); break;
-        case 3: gemv_wait_vmcnt<3>(); break;
-        case 4: gemv_wait_vmcnt<4>(); break;
-        case 5: gemv_wait_vmcnt<5>(); break;
-        case 6: gemv_wait_vmcnt<6>(); break;
-        default: gemv_wait_vmcnt<7>(); break;
-    }
-}
-
-template <int F, int U, int WPB, bool RAG>
-__global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *__restrict__ x,
-                                                      const uint8_t *__restrict__ codes,
-                                                      const float *__restrict__ scales, uint32_t N, uint32_t K,
-                                                      uint32_t R, uint16_t *__restrict__ y) {
-    static_assert(U >= 1 && U <= 7, "gemv_wait_upto covers up to 7 loads in flight");
-    extern __shared__ __attribute__((aligned(16))) uint32_t xs_words[];
-    uint8_t *xs = reinterpret_cast<uint8_t *>(xs_words);   // the activation, K bf16
-    const int tid = threadIdx.x, lane = tid & 63;
-    const uint32_t w = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t cpr = (K + 1023) >> 10;            // 1 KB chunks per row
-    const uint32_t spr = (cpr + U - 1) / U;           // steps per row (the last may be short)
+template <int F, int CPR, int WPB>
+// (No __restrict__ on the inputs: loads through a restrict pointer to const may
+// be treated as invariant and moved across the compiler barriers that fix the
+// issue order.)
+__global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *x, const uint8_t *codes,
+                                                      const float *scales, uint32_t N, uint32_t K,
+                                                      uint16_t *__restrict__ y) {
+    constexpr uint32_t XMAX = CPR * 128;                             // 16-byte activation pieces at most
+    constexpr uint32_t XPT = (XMAX + 64 * WPB - 1) / (64 * WPB);     // pieces per thread
+    __shared__ __attribute__((aligned(16))) u32x4 xs[XMAX];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t n = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nr = n < N ? n : N - 1;   // a wave past the last row reads row N - 1, stores nothing
+    const uint32_t xp = K / 8;               // 16-byte activation pieces
     const uint32_t live = (K & 1023) ? (K & 1023) >> 4 : 64;   // lanes of the last chunk inside the row
-    const uint32_t r0 = w * R;
-    const uint32_t rows = r0 < N ? (N - r0 < R ? N - r0 : R) : 0;
-    const uint8_t *wbase = codes + (size_t)(r0 < N ? r0 : 0) * K;   // this wave's rows, R K contiguous bytes
-
-    // In issue order (the waits count on it): this lane's row scale (lane j
-    // holds row r0 + j, R <= 64), the activation copies, the first step.
-    const float sraw = gemv_load4(scales && rows ? static_cast<const void *>(scales + r0 + ((uint32_t)lane < rows ? lane : 0))
-                                                 : static_cast<const void *>(codes));
-    // Activation: piece i (8 bf16, 16 bytes) by thread i mod 64 WPB.
-    for (uint32_t i = tid; i < K / 8; i += 64 * WPB) dma16(x + 8 * (size_t)i, xs + 16 * (size_t)(i - lane));
-
-    // Step j of row r: chunks [j U, min((j + 1) U, cpr)) of the row; steps never
-    // span two rows, so a row ends with its last step.
-    auto step_loads = [&](uint32_t r, uint32_t j) -> uint32_t {   // chunks the step holds (0: none)
-        if (r >= rows) return 0;
-        const uint32_t left = cpr - j * U;
-        return left < U ? left : U;
-    };
-    auto issue = [&](u32x4 (&q)[U], uint32_t r, uint32_t j) {
-        const uint32_t n = step_loads(r, j);
-        const uint32_t base = r * K + j * U * 1024;
+    const float sv = scales ? scales[nr] : 1.0f;
+    const u32x4 *x16 = reinterpret_cast<const u32x4 *>(x);
+    u32x4 xt[XPT];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if ((uint32_t)u < n) {
-                const bool lastc = RAG && j * U + u + 1 == cpr;
-                const uint32_t lanec = lastc && (uint32_t)lane >= live ? live - 1 : lane;
-                q[u] = gemv_load16(wbase, base + u * 1024 + 16 * lanec);
-            }
-        }
-    };
-
-    uint32_t r = 0, j = 0;                            // the step being consumed
-    float a0 = 0.0f, a1 = 0.0f;
-    float sv = 1.0f;
-    // One step: n chunks (n == U: no guard), then the row's end when j is its
-    // last step.
-    auto consume = [&](const u32x4 (&q)[U], uint32_t n) {
-        const uint8_t *xrow = xs + 2 * ((size_t)j * U * 1024 + 16 * lane);
-        auto chunk = [&](int u) {
-            uint32_t wv[8];
-            decode16<F>(q[u], wv);
-            const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow + u * 2048);
-            u32x4 xa, xb;
-            if (RAG && j * U + u + 1 == cpr && (uint32_t)lane >= live) {
-                // Past K in a ragged last chunk: no codes, and no activation
-                // past the LDS copy either.
-#pragma unroll
-                for (int i = 0; i < 8; ++i) wv[i] = 0u;
-                xa = xb = u32x4{0u, 0u, 0u, 0u};
-            } else {
-                xa = xp[0];
-                xb = xp[1];
-            }
-            a0 = dot2(wv[0], xa.x, a0);
-            a1 = dot2(wv[1], xa.y, a1);
-            a0 = dot2(wv[2], xa.z, a0);
-            a1 = dot2(wv[3], xa.w, a1);
-            a0 = dot2(wv[4], xb.x, a0);
-            a1 = dot2(wv[5], xb.y, a1);
-            a0 = dot2(wv[6], xb.z, a0);
-            a1 = dot2(wv[7], xb.w, a1);
-        };
-        if (n == U) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) chunk(u);
-        } else {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if ((uint32_t)u < n) chunk(u);
-        }
-        if (j + 1 == spr) {   // the row's last step
-            const float t = wave_sum_dpp(a0 + a1);
-            const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), r));
-            if (lane == 0) y[r0 + r] = (uint16_t)f32_to_bf16_bits(t * s);
-            a0 = a1 = 0.0f;
-            j = 0;
-            ++r;
-        } else {
-            ++j;
-        }
-    };
-    auto next_of = [&](uint32_t rr, uint32_t jj, uint32_t &rn, uint32_t &jn) {
-        if (jj + 1 == spr) {
-            rn = rr + 1;
-            jn = 0;
-        } else {
-            rn = rr;
-            jn = jj + 1;
-        }
-    };
-
-    // Two register sets, used in turn: step s + 1 is requested before step s
-    // is waited for and consumed (requesting two steps ahead, or a wave's
-    // whole rows at once, measured slower: more of the matrix in flight at
-    // the start of the launch); nothing is requested past the wave's rows.
-    u32x4 qa[U], qb[U];
-    issue(qa, 0, 0);
-    gemv_wait_upto(step_loads(0, 0));   // the scale and the activation copies have landed
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    sv = scales ? sraw : 1.0f;
-    while (r < rows) {
-        uint32_t rn, jn;
-        next_of(r, j, rn, jn);
-        const uint32_t na = step_loads(r, j), nb = step_loads(rn, jn);
-        issue(qb, rn, jn);
-        gemv_wait_upto(nb);   // qa's step has landed; qb's may still be in flight
-        gemv_after_wait(qa);
-        consume(qa, na);
-        if (r >= rows) break;
-        next_of(r, j, rn, jn);
-        const uint32_t nb2 = step_loads(r, j), na2 = step_loads(rn, jn);
-        issue(qa, rn, jn);
-        gemv_wait_upto(na2);
-        gemv_after_wait(qb);
-        consume(qb, nb2);
+    for (uint32_t j = 0; j < XPT; ++j) {
+        const uint32_t i = tid + j * 64 * WPB;
+        xt[j] = x16[i < xp ? i : xp - 1];
     }
+    // The codes are requested after the scale and the activation.
+    asm volatile("" ::: "memory");
+    const u32x4 *wr = reinterpret_cast<const u32x4 *>(codes + (size_t)nr * K);
+    u32x4 q[CPR];
+#pragma unroll
+    for (int c = 0; c < CPR; ++c) {
+        const uint32_t lc = c == CPR - 1 && lane >= live ? live - 1 : lane;
+        q[c] = __builtin_nontemporal_load(wr + 64 * c + lc);
+        asm volatile("" ::: "memory");   // issued in chunk order, the order they are consumed in
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < XPT; ++j) {
+        const uint32_t i = tid + j * 64 * WPB;
+        if (i < xp) xs[i] = xt[j];
+    }
+    lds_sync();
+    // Past K in a ragged last chunk: no codes, and no activation past the LDS
+    // copy either (a mask, not a branch, so the waits stay per chunk).
+    const uint32_t keep_last = lane < live ? ~0u : 0u;
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPR; ++c) {
+        uint32_t wv[8];
+        decode16<F>(q[c], wv);
+        u32x4 xa = xs[128 * c + 2 * lane], xb = xs[128 * c + 2 * lane + 1];
+        if (c == CPR - 1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wv[i] &= keep_last;
+            xa &= keep_last;
+            xb &= keep_last;
+        }
+        a0 = dot2(wv[0], xa.x, a0);
+        a1 = dot2(wv[1], xa.y, a1);
+        a0 = dot2(wv[2], xa.z, a0);
+        a1 = dot2(wv[3], xa.w, a1);
+        a0 = dot2(wv[4], xb.x, a0);
+        a1 = dot2(wv[5], xb.y, a1);
+        a0 = dot2(wv[6], xb.z, a0);
+        a1 = dot2(wv[7], xb.w, a1);
+    }
+    const float t = wave_sum_dpp(a0 + a1);
+    if (lane == 0 && n < N) y[n] = (uint16_t)f32_to_bf16_bits(t * sv);
 }
 
 // ------------------------------------------------------------------ read yardstick
@@ -894,44 +789,42 @@ int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *sca
                                                               0.0f, st);
 }
 
-// gemv_rows's launch: about 28 waves per CU (one round: every wave resident)
-// with R = ceil(N / waves) consecutive rows each, at most 64; 7-chunk steps
-// when rows split into whole groups of 7 KB (K = 14336), else 4; 8-wave
-// workgroups for rows of 8 KB or more (one activation copy per 8 waves), else 4.
+// gemv_rows' launch: one wave per row, 4-wave blocks for rows of up to 8 KB
+// when there are more than 16 rows per CU, else 8-wave blocks (fewer copies
+// of a long activation per CU): [14336, 4096] 10.12 us with 4-wave blocks
+// against 10.25 with 8, [4096, 4096] 4.54 against 4.46.
+template <int F, int CPR>
+int launch_gemv_rows_c(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                       uint16_t *y, hipStream_t st) {
+    if (CPR <= 8 && N > (uint32_t)device_props().cus * 16)
+        hipLaunchKernelGGL((gemv_rows<F, CPR, 4>), dim3((N + 3) / 4), dim3(256), 0, st, x, codes, scales, N, K, y);
+    else
+        hipLaunchKernelGGL((gemv_rows<F, CPR, 8>), dim3((N + 7) / 8), dim3(512), 0, st, x, codes, scales, N, K, y);
+    return check_launch("gemv_rows");
+}
+
+// Rows of 2..16 KB (1024 < K <= 16384); the caller sends the rest to gemv_w8a16.
 template <int F>
 int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                      uint16_t *y, hipStream_t st) {
-    const uint32_t cpr = (K + 1023) / 1024;
-    const bool rag = (K & 1023) != 0;
-    // Waves per CU that stay resident: 8 per SIMD for the 4-chunk form
-    // (61 VGPRs), 5 for the 7-chunk and ragged forms (87-89 VGPRs).
-    const uint32_t per_cu = (cpr % 7 != 0 && !rag) ? 28 : 20;
-    const uint32_t target = (uint32_t)device_props().cus * per_cu;
-    uint32_t R = (N + target - 1) / target;
-    R = R < 1 ? 1 : R > 64 ? 64 : R;
-    const uint32_t waves = (N + R - 1) / R;
-    const size_t lds = (size_t)K * 2;
-#define RENG_ROWS(UU, WW, RG)                                                                                    \
-    hipLaunchKernelGGL((gemv_rows<F, UU, WW, RG>), dim3((waves + WW - 1) / WW), dim3(64 * WW), lds, st, x, codes, \
-                       scales, N, K, R, y)
-    if (cpr % 7 == 0 && !rag) RENG_ROWS(7, 8, false);
-    else if (cpr >= 8) {
-        if (rag) RENG_ROWS(4, 8, true);
-        else RENG_ROWS(4, 8, false);
-    } else {
-        if (rag) RENG_ROWS(4, 4, true);
-        else RENG_ROWS(4, 4, false);
-    }
+    switch ((K + 1023) / 1024) {
+#define RENG_ROWS(C) \
+    case C: return launch_gemv_rows_c<F, C>(x, codes, scales, N, K, y, st);
+        RENG_ROWS(2) RENG_ROWS(3) RENG_ROWS(4) RENG_ROWS(5) RENG_ROWS(6) RENG_ROWS(7) RENG_ROWS(8) RENG_ROWS(9)
+        RENG_ROWS(10) RENG_ROWS(11) RENG_ROWS(12) RENG_ROWS(13) RENG_ROWS(14) RENG_ROWS(15) RENG_ROWS(16)
 #undef RENG_ROWS
-    return check_launch("gemv_rows");
+        default:
+            set_error("gemv_rows: K = %u outside 1025..16384", K);
+            return RENG_HIP_EINVAL;
+    }
 }
 
 template <int F>
 int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
-    // One activation row: the contiguous-rows GEMV while the row fits in LDS
-    // (64 KB); x and codes are 16-byte aligned (checked by the entry point).
-    if (M == 1 && K <= 32768)
+    // One activation row of 1 to 16 KB: a wave per row with the whole row in
+    // flight; x and codes are 16-byte aligned (checked by the entry point).
+    if (M == 1 && K > 1024 && K <= 16384)
         return launch_gemv_rows<F>(x, codes, scales, N, K, y, st);
     // More than 64 rows: output tiles on the bf16 MFMA, each code tile read
     // once per 64-256 activation rows (the 64-row loop below re-reads every

@@ -345,6 +345,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
                 // Partials and counter go through agent-scope (device-coherent)
                 // accesses, which bypass the per-XCD L2s' non-coherent copies;
                 // the stores have completed (vmcnt 0) before the count moves.
+                // The count is an acquire-release: the block's stores (ordered
+                // before it by the barrier) happen before the last block's
+                // reads (ordered after its own count by the next barrier).
                 float *mine = slot_ptr(blockIdx.x, t);
 #pragma unroll
                 for (int q = 0; q < NQ; ++q)
@@ -355,7 +358,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
                 wait_vmcnt<0>();
                 __syncthreads();
                 if (tid == 0) {
-                    const uint32_t seen = __hip_atomic_fetch_add(cnt + t, 1u, __ATOMIC_RELAXED,
+                    const uint32_t seen = __hip_atomic_fetch_add(cnt + t, 1u, __ATOMIC_ACQ_REL,
                                                                  __HIP_MEMORY_SCOPE_AGENT);
                     last_flag = seen + 1 == b1 - b0 + 1;
                 }

@@ -38,7 +38,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // s_waitcnt lgkmcnt(0): the wave's LDS reads (and scalar loads) are done.
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14)); }
+__device__ __forceinline__ void wait_lgkm0() {
+    asm volatile("" ::: "memory");   // LDS accesses before the wait stay before it
+    __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14));
+    asm volatile("" ::: "memory");
+}
 
 // One global_load_lds_dwordx4: 16 bytes per lane from
 // g into LDS at l + 16 * lane (l is wave-uniform). A __device__ function

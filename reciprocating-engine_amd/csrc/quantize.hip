@@ -486,31 +486,36 @@ int launch_quantize_group(const QBatch &b, int dtype, int format, int scheme, fl
     const float full = maxf * backoff;
     const float *fs = nullptr;
     const uint32_t *fb = nullptr;
+    uint32_t *ws = nullptr;   // the HW scheme's tensor maxima, scales and biases
     if (scheme == RENG_HIP_HW) {
-        uint32_t *ws = nullptr;
         RENG_CHECK_HIP(hipMallocAsync(reinterpret_cast<void **>(&ws), 3 * QBATCH * sizeof(uint32_t), st));
         uint32_t *tmax = ws;
         float *scl = reinterpret_cast<float *>(ws + QBATCH);
         uint32_t *bias = ws + 2 * QBATCH;
         hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(QBATCH), 0, st, tmax, QBATCH);
         int rc = check_launch("zero");
-        if (rc) return rc;
-        rc = dtype == RENG_HIP_BF16 ? launch_absmax<uint16_t>(b, nullptr, tmax, st)
-                                    : launch_absmax<float>(b, nullptr, tmax, st);
-        if (rc) return rc;
-        if (dtype == RENG_HIP_BF16) {
-            if (format == RENG_HIP_E4M3)
-                hipLaunchKernelGGL((hw_bias_kernel<uint16_t, RENG_HIP_E4M3>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
-            else
-                hipLaunchKernelGGL((hw_bias_kernel<uint16_t, RENG_HIP_E5M2>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
-        } else {
-            if (format == RENG_HIP_E4M3)
-                hipLaunchKernelGGL((hw_bias_kernel<float, RENG_HIP_E4M3>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
-            else
-                hipLaunchKernelGGL((hw_bias_kernel<float, RENG_HIP_E5M2>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
+        if (rc == RENG_HIP_OK)
+            rc = dtype == RENG_HIP_BF16 ? launch_absmax<uint16_t>(b, nullptr, tmax, st)
+                                        : launch_absmax<float>(b, nullptr, tmax, st);
+        if (rc == RENG_HIP_OK) {
+            if (dtype == RENG_HIP_BF16) {
+                if (format == RENG_HIP_E4M3)
+                    hipLaunchKernelGGL((hw_bias_kernel<uint16_t, RENG_HIP_E4M3>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
+                else
+                    hipLaunchKernelGGL((hw_bias_kernel<uint16_t, RENG_HIP_E5M2>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
+            } else {
+                if (format == RENG_HIP_E4M3)
+                    hipLaunchKernelGGL((hw_bias_kernel<float, RENG_HIP_E4M3>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
+                else
+                    hipLaunchKernelGGL((hw_bias_kernel<float, RENG_HIP_E5M2>), dim3(1), dim3(QBATCH), 0, st, b, tmax, backoff, scl, bias);
+            }
+            rc = check_launch("hw_bias");
         }
-        rc = check_launch("hw_bias");
-        if (rc) return rc;
+        if (rc != RENG_HIP_OK) {
+            // Ordered after whatever of the above was enqueued; the launch error is the one reported.
+            (void)hipFreeAsync(ws, st);
+            return rc;
+        }
         fs = scl;
         fb = bias;
     }
@@ -529,9 +534,9 @@ int launch_quantize_group(const QBatch &b, int dtype, int format, int scheme, fl
                  ? launch_group<float, RENG_HIP_E4M3>(b, key, scheme, full, clamp, fs, fb, st)
                  : launch_group<float, RENG_HIP_E5M2>(b, key, scheme, full, clamp, fs, fb, st);
     }
-    if (fs) {
-        // The partials were allocated on this stream; the free is ordered after the encode.
-        const hipError_t e = hipFreeAsync(const_cast<float *>(fs) - QBATCH, st);
+    if (ws) {
+        // Allocated on this stream: the free is ordered after the encode.
+        const hipError_t e = hipFreeAsync(ws, st);
         if (rc == RENG_HIP_OK && e != hipSuccess) {
             set_error("hipFreeAsync: %s", hipGetErrorString(e));
             rc = RENG_HIP_EDEVICE;

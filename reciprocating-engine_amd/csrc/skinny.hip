@@ -71,7 +71,11 @@ __device__ __forceinline__ void copy16(const uint8_t *g, uint8_t *l) {
 
 // s_waitcnt lgkmcnt(0): this wave's LDS reads have returned, so copies may
 // overwrite the slot they read.
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14)); }
+__device__ __forceinline__ void wait_lgkm0() {
+    asm volatile("" ::: "memory");   // LDS accesses before the wait stay before it
+    __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (0 << 8) | (3 << 14));
+    asm volatile("" ::: "memory");
+}
 
 // A workgroup barrier without the vmcnt(0) of __syncthreads' fence; the memory
 // clobbers keep LDS accesses on their side of it.

@@ -96,3 +96,34 @@ def test_rotation_exceeds_the_infinity_cache():
         assert n >= 4
         assert n * nbytes >= 2 * bench.MALL_BYTES or n == 1024
     assert bench.MALL_BYTES == 256 << 20
+
+
+class FakeOracle:
+    """quantize_with returns a token per matrix; split follows reng-fp8's rule
+    (one thread per 2^20 elements, capped at 8 and at rows)."""
+
+    def __init__(self):
+        self.calls = 0
+
+    def quantize_with(self, w, rows, cols, fmt, scheme, backoff, thread_cap=8):
+        self.calls += 1
+        return ("q", rows, cols, self.calls)
+
+    @staticmethod
+    def split(rows, cols):
+        return max(1, min(8, (rows * cols) >> 20, rows))
+
+
+def test_cpu_baseline_is_the_median_of_three_runs(monkeypatch):
+    O = FakeOracle()
+    host = [(4096, 4096, None), (1024, 4096, None)]
+    ticks = iter([0.0, 5.0, 5.0, 7.0, 7.0, 13.0])   # runs of 5, 2 and 6 s
+    monkeypatch.setattr(bench.time, "perf_counter", lambda: next(ticks))
+    refs, secs = bench.time_oracle_sample(O, host, "e4m3")
+    assert secs == [5.0, 2.0, 6.0]
+    assert [r[3] for r in refs] == [1, 2]           # the first run's results are the ones kept
+    rec = bench.cpu_record(O, host, secs, "two matrices")
+    nbytes = bench.quant_bytes(4096, 4096) + bench.quant_bytes(1024, 4096)
+    assert rec["value"] == pytest.approx(round(nbytes / 5.0 / 1e9, 3))   # median 5 s
+    assert rec["cores"] == 8 and rec["kind"] == "port" and rec["unit"] == "GB/s"
+    assert "median of 3 runs" in rec["sample"]
