@@ -458,10 +458,11 @@ def bench_qwen32b_quantize(torch, R, fmt="e4m3", steps=3, warmup=1, parity=True)
 
 def bench_host_quantize(torch, R, layers=2, fmt="e4m3"):
     """The host-pointer entry Rust's quantize_with calls (reng_hip_quantize_host:
-    pinned row chunks over two streams, upload, quantize and download
-    overlapped): Llama-3.1-8B layers 0..layers-1 from host memory, codes and
-    scales back in host memory. GB/s of the same algorithmic bytes, PCIe
-    included (never the headline value)."""
+    4 MB row chunks through three pinned slots and streams, host copies in and
+    out on thread pools, uploads, quantizes and downloads overlapped):
+    Llama-3.1-8B layers 0..layers-1 from host memory, codes and scales back in
+    host memory. GB/s of the same algorithmic bytes, PCIe included (never the
+    headline value), beside pinned-memory PCIe copies as the yardstick."""
     import numpy as np
 
     gen = torch.Generator(device="cuda")
@@ -471,14 +472,58 @@ def bench_host_quantize(torch, R, layers=2, fmt="e4m3"):
         for name, rows, cols in LLAMA_8B:
             mats.append((rows, cols, make_bf16(torch, rows, cols, gen).cpu().numpy().view(np.uint16)))
     R.quantize_host(mats[0][2], mats[0][0], mats[0][1], fmt, "pcs")   # staging buffers, first touch
-    t0 = time.perf_counter()
-    for rows, cols, w in mats:
-        R.quantize_host(w, rows, cols, fmt, "pcs")
-    secs = time.perf_counter() - t0
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for rows, cols, w in mats:
+            R.quantize_host(w, rows, cols, fmt, "pcs")
+        runs.append(time.perf_counter() - t0)
+    secs = sorted(runs)[1]
     nbytes = sum(quant_bytes(r, c) for r, c, _ in mats)
+    elems = sum(r * c for r, c, _ in mats)
     return {"matrices": len(mats), "algorithmic_bytes": nbytes, "secs": round(secs, 4),
+            "runs_s": [round(t, 4) for t in runs],
             "GBps": round(nbytes / secs / 1e9, 2), "layers": layers, "format": fmt,
-            "note": "host memory in and out, PCIe and host copies included"}
+            "upload_GBps": round(2 * elems / secs / 1e9, 2), "download_GBps": round(elems / secs / 1e9, 2),
+            "pcie": pcie_yardstick(torch),
+            "note": "host memory in and out, PCIe and host copies included; the median of 3 passes; "
+                    "upload / download = the bf16 weights / the codes over the whole pass"}
+
+
+def pcie_yardstick(torch, nbytes=256 << 20):
+    """Pinned host <-> device copies of nbytes, each direction alone and both at
+    once (torch copies on two streams): GB/s, the best of 3."""
+    h_in = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    h_out = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    d_in = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    d_out = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def best(fn):
+        ts = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return min(ts)
+
+    def up():
+        with torch.cuda.stream(s1):
+            d_in.copy_(h_in, non_blocking=True)
+
+    def down():
+        with torch.cuda.stream(s2):
+            h_out.copy_(d_out, non_blocking=True)
+
+    def both():
+        up()
+        down()
+
+    tu, td, tb = best(up), best(down), best(both)
+    return {"bytes": nbytes, "h2d_GBps": round(nbytes / tu / 1e9, 1), "d2h_GBps": round(nbytes / td / 1e9, 1),
+            "both_GBps": round(2 * nbytes / tb / 1e9, 1)}
 
 
 def bench_decode_step(layers=4, positions=512):

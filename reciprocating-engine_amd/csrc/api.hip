@@ -17,6 +17,7 @@
 #include "common.h"
 #include "gemm.h"
 #include "quantize.h"
+#include "staging.h"
 
 namespace reng {
 
@@ -178,195 +179,13 @@ RENG_HIP_API int reng_hip_quantize_batch(const reng_hip_matrix *mats, size_t n, 
     return RENG_HIP_OK;
 }
 
-namespace {
-
-// Host staging for reng_hip_quantize_host: pinned host chunks (hipHostMalloc)
-// and two streams per device, kept for the life of the process with
-// grow-only device buffers. A matrix moves in row chunks of about
-// STAGE_CHUNK bytes: the CPU copies chunk i + 1 into one pinned buffer while
-// chunk i's upload, quantize and download run on the other slot's stream, so
-// the uploads, the kernels and the downloads of neighbouring chunks overlap.
-constexpr size_t STAGE_CHUNK = (size_t)16 << 20;
-
-struct HostStage {
-    std::mutex mu;
-    bool ready = false;
-    hipStream_t st[2] = {nullptr, nullptr};
-    hipEvent_t up[2] = {nullptr, nullptr};     // slot's pinned input may be reused
-    hipEvent_t down[2] = {nullptr, nullptr};   // slot's pinned output holds its chunk
-    hipEvent_t all_up = nullptr, quantized = nullptr;
-    void *pin_in[2] = {nullptr, nullptr};
-    void *pin_out[2] = {nullptr, nullptr};
-    void *dw = nullptr;
-    size_t dw_cap = 0;
-    uint8_t *dc = nullptr;
-    size_t dc_cap = 0;
-    float *ds = nullptr;   // rows scales, then the exponent bias (one u32)
-    size_t ds_cap = 0;
-};
-
-HostStage &host_stage(int dev) {
-    static std::mutex mu;
-    static std::map<int, std::unique_ptr<HostStage>> stages;
-    std::lock_guard<std::mutex> lk(mu);
-    auto &p = stages[dev];
-    if (!p) p.reset(new HostStage());
-    return *p;
-}
-
-// memcpy over up to 8 host threads for large copies (a single thread copies
-// pageable memory well below the PCIe rate).
-void par_copy(void *dst, const void *src, size_t n) {
-    const size_t min_piece = (size_t)2 << 20;
-    size_t t = std::min<size_t>(8, std::max<size_t>(1, std::thread::hardware_concurrency() / 2));
-    t = std::min(t, std::max<size_t>(1, n / min_piece));
-    if (t <= 1) {
-        memcpy(dst, src, n);
-        return;
-    }
-    const size_t piece = (n + t - 1) / t;
-    std::vector<std::thread> th;
-    for (size_t i = 1; i < t; ++i) {
-        const size_t a = i * piece, b = std::min(n, a + piece);
-        if (a < b) th.emplace_back([=] { memcpy(static_cast<char *>(dst) + a, static_cast<const char *>(src) + a, b - a); });
-    }
-    memcpy(dst, src, std::min(n, piece));
-    for (auto &x : th) x.join();
-}
-
-int grow(void **p, size_t *cap, size_t bytes) {
-    if (*cap >= bytes) return RENG_HIP_OK;
-    if (*p) RENG_CHECK_HIP(hipFree(*p));
-    *p = nullptr;
-    *cap = 0;
-    RENG_CHECK_HIP(hipMalloc(p, bytes));
-    *cap = bytes;
-    return RENG_HIP_OK;
-}
-
-int stage_init(HostStage &S) {
-    if (S.ready) return RENG_HIP_OK;
-    for (int i = 0; i < 2; ++i) {
-        if (!S.st[i]) RENG_CHECK_HIP(hipStreamCreateWithFlags(&S.st[i], hipStreamNonBlocking));
-        if (!S.up[i]) RENG_CHECK_HIP(hipEventCreateWithFlags(&S.up[i], hipEventDisableTiming));
-        if (!S.down[i]) RENG_CHECK_HIP(hipEventCreateWithFlags(&S.down[i], hipEventDisableTiming));
-        if (!S.pin_in[i]) RENG_CHECK_HIP(hipHostMalloc(&S.pin_in[i], STAGE_CHUNK, hipHostMallocDefault));
-        if (!S.pin_out[i]) RENG_CHECK_HIP(hipHostMalloc(&S.pin_out[i], STAGE_CHUNK, hipHostMallocDefault));
-    }
-    if (!S.all_up) RENG_CHECK_HIP(hipEventCreateWithFlags(&S.all_up, hipEventDisableTiming));
-    if (!S.quantized) RENG_CHECK_HIP(hipEventCreateWithFlags(&S.quantized, hipEventDisableTiming));
-    S.ready = true;
-    return RENG_HIP_OK;
-}
-
-// The staged quantize of one host matrix (arguments already checked).
-int quantize_staged(HostStage &S, const void *w, int dtype, size_t rows, size_t cols, int format, int scaling,
-                    float backoff, uint8_t *codes, float *scales, uint32_t *exp_bias) {
-    if (int rc = stage_init(S)) return rc;
-    const size_t esz = dtype_bytes(dtype);
-    const size_t row_bytes = cols * esz;
-    if (int rc = grow(&S.dw, &S.dw_cap, rows * row_bytes)) return rc;
-    if (int rc = grow(reinterpret_cast<void **>(&S.dc), &S.dc_cap, rows * cols)) return rc;
-    if (int rc = grow(reinterpret_cast<void **>(&S.ds), &S.ds_cap, (rows + 1) * sizeof(float))) return rc;
-    uint32_t *dbias = reinterpret_cast<uint32_t *>(S.ds + rows);
-    // Rows per chunk: the input chunk fits a pinned buffer (codes are smaller).
-    const size_t rpc = std::max<size_t>(1, STAGE_CHUNK / row_bytes);
-    const size_t chunks = (rows + rpc - 1) / rpc;
-    const bool per_row = scaling != RENG_HIP_HW;   // PCS and UNIT quantize rows independently
-    if (row_bytes > STAGE_CHUNK) {
-        // A single row larger than a pinned buffer: unpipelined copies.
-        RENG_CHECK_HIP(hipMemcpy(S.dw, w, rows * row_bytes, hipMemcpyHostToDevice));
-        int rc = reng_hip_quantize(S.dw, dtype, rows, cols, cols, format, scaling, backoff, S.dc, S.ds, dbias,
-                                   S.st[0]);
-        if (rc) return rc;
-        RENG_CHECK_HIP(hipStreamSynchronize(S.st[0]));
-        RENG_CHECK_HIP(hipMemcpy(codes, S.dc, rows * cols, hipMemcpyDeviceToHost));
-        RENG_CHECK_HIP(hipMemcpy(scales, S.ds, rows * sizeof(float), hipMemcpyDeviceToHost));
-        if (exp_bias) RENG_CHECK_HIP(hipMemcpy(exp_bias, dbias, sizeof(uint32_t), hipMemcpyDeviceToHost));
-        return RENG_HIP_OK;
-    }
-    auto range = [&](size_t i, size_t &r0, size_t &nr) {
-        r0 = i * rpc;
-        nr = std::min(rpc, rows - r0);
-    };
-    // Chunk i's codes, downloaded into pin_out[i & 1], copied out once landed.
-    auto copy_out = [&](size_t i) -> int {
-        size_t r0, nr;
-        range(i, r0, nr);
-        RENG_CHECK_HIP(hipEventSynchronize(S.down[i & 1]));
-        par_copy(codes + r0 * cols, S.pin_out[i & 1], nr * cols);
-        return RENG_HIP_OK;
-    };
-    auto download = [&](size_t i) -> int {
-        size_t r0, nr;
-        range(i, r0, nr);
-        const int k = (int)(i & 1);
-        if (i >= 2)
-            if (int rc = copy_out(i - 2)) return rc;   // the slot's output buffer is free again
-        RENG_CHECK_HIP(hipMemcpyAsync(S.pin_out[k], S.dc + r0 * cols, nr * cols, hipMemcpyDeviceToHost, S.st[k]));
-        RENG_CHECK_HIP(hipEventRecord(S.down[k], S.st[k]));
-        return RENG_HIP_OK;
-    };
-    for (size_t i = 0; i < chunks; ++i) {
-        size_t r0, nr;
-        range(i, r0, nr);
-        const int k = (int)(i & 1);
-        if (i >= 2) RENG_CHECK_HIP(hipEventSynchronize(S.up[k]));   // the slot's pinned input is free
-        par_copy(S.pin_in[k], static_cast<const char *>(w) + r0 * row_bytes, nr * row_bytes);
-        char *dst = static_cast<char *>(S.dw) + r0 * row_bytes;
-        RENG_CHECK_HIP(hipMemcpyAsync(dst, S.pin_in[k], nr * row_bytes, hipMemcpyHostToDevice, S.st[k]));
-        RENG_CHECK_HIP(hipEventRecord(S.up[k], S.st[k]));
-        if (per_row) {
-            int rc = reng_hip_quantize(dst, dtype, nr, cols, cols, format, scaling, backoff, S.dc + r0 * cols,
-                                       S.ds + r0, nullptr, S.st[k]);
-            if (rc) return rc;
-            if ((rc = download(i))) return rc;
-        }
-    }
-    if (!per_row) {
-        // HW: one exponent bias from the whole matrix, so every chunk is on the
-        // device before the quantize; then the downloads alternate again.
-        RENG_CHECK_HIP(hipEventRecord(S.all_up, S.st[1]));
-        RENG_CHECK_HIP(hipStreamWaitEvent(S.st[0], S.all_up, 0));
-        int rc = reng_hip_quantize(S.dw, dtype, rows, cols, cols, format, scaling, backoff, S.dc, S.ds, dbias,
-                                   S.st[0]);
-        if (rc) return rc;
-        RENG_CHECK_HIP(hipEventRecord(S.quantized, S.st[0]));
-        RENG_CHECK_HIP(hipStreamWaitEvent(S.st[1], S.quantized, 0));
-        for (size_t i = 0; i < chunks; ++i)
-            if ((rc = download(i))) return rc;
-    }
-    for (size_t i = chunks >= 2 ? chunks - 2 : 0; i < chunks; ++i)
-        if (int rc = copy_out(i)) return rc;
-    RENG_CHECK_HIP(hipStreamSynchronize(S.st[0]));
-    RENG_CHECK_HIP(hipStreamSynchronize(S.st[1]));
-    RENG_CHECK_HIP(hipMemcpy(scales, S.ds, rows * sizeof(float), hipMemcpyDeviceToHost));
-    if (exp_bias) {
-        if (per_row) *exp_bias = format == RENG_HIP_E4M3 ? 7u : 15u;   // the format's own bias (lib.rs:544, 550)
-        else RENG_CHECK_HIP(hipMemcpy(exp_bias, dbias, sizeof(uint32_t), hipMemcpyDeviceToHost));
-    }
-    return RENG_HIP_OK;
-}
-
-}  // namespace
-
 RENG_HIP_API int reng_hip_quantize_host(const void *w, int dtype, size_t rows, size_t cols,
                                         int format, int scaling, float backoff, uint8_t *codes,
                                         float *scales, uint32_t *exp_bias) {
     clear_error();
-    int rc = check_quantize_args(w, dtype, rows, cols, cols, format, scaling, backoff, codes, scales);
+    const int rc = check_quantize_args(w, dtype, rows, cols, cols, format, scaling, backoff, codes, scales);
     if (rc) return rc;
-    int dev = 0;
-    RENG_CHECK_HIP(hipGetDevice(&dev));
-    HostStage &S = host_stage(dev);
-    std::lock_guard<std::mutex> lk(S.mu);   // one staged call per device at a time
-    rc = quantize_staged(S, w, dtype, rows, cols, format, scaling, backoff, codes, scales, exp_bias);
-    if (rc) {
-        // Leave the staging streams idle for the next call.
-        (void)hipStreamSynchronize(S.st[0]);
-        (void)hipStreamSynchronize(S.st[1]);
-    }
-    return rc;
+    return quantize_host_staged(w, dtype, rows, cols, format, scaling, backoff, codes, scales, exp_bias);
 }
 
 RENG_HIP_API int reng_hip_row_absmax(const void *w, int dtype, size_t rows, size_t cols, size_t ld,

@@ -387,12 +387,14 @@ def test_rows_whose_scale_is_subnormal(R, fmt):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_the_staged_host_entry_over_many_chunks(R, dtype):
-    """reng_hip_quantize_host moves a matrix in pinned row chunks over two
-    streams: matrices of 1, several and a ragged number of chunks (16 MB of
-    input each), every scheme, bit for bit against the oracle, twice in a row
-    (the staging buffers are kept and reused)."""
+    """reng_hip_quantize_host moves a matrix in 4 MB row chunks through three
+    pinned slots and streams, with thread pools copying in and out: matrices of
+    one chunk, of more chunks than slots with a ragged last one, of one row per
+    chunk, and (f32) of rows larger than a slot (the unpipelined path); every
+    scheme, bit for bit against the oracle, twice in a row (the staging buffers
+    and threads are kept and reused)."""
     rng = np.random.default_rng(71)
-    for rows, cols in [(64, 4096), (4100, 4096), (2304, 14336)]:
+    for rows, cols in [(64, 4096), (4100, 4096), (2304, 14336), (3, 1048592)]:
         x = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
         w = bf16_bits(x).ravel() if dtype == "bf16" else x.ravel()
         for fmt, sc in ((E4M3, "pcs"), (E5M2, "hw"), (E4M3, "unit"), (E4M3, "hw")):
