@@ -3,7 +3,9 @@ the C ABI it must give what reng_hip_gemm_w8a16 gives, bit for bit, on two
 calls in a row (the second smaller, so it runs on what the first left in the
 shared static scratch), on products that use the split-K scratch (16 < M <= 64
 with K splits, M > 64 in 64-row tiles), the stream-K partials and tile
-counters (long-K M > 64 over few tiles) and on ones that do not."""
+counters (long-K M > 64 over few tiles) and on ones that do not; and captured
+into a hipGraph on a fresh stream, where the allocating entry refuses to grow
+its per-stream buffers, with every replay equal to the eager result."""
 import ctypes
 
 import numpy as np
@@ -68,3 +70,40 @@ def test_noalloc_refuses_what_the_allocating_entry_refuses(R):
     assert L.reng_hip_gemm_w8a16_noalloc(p, p, None, 1, 8, 40, E4M3, p, None) == R.EINVAL
     assert b"multiple of 16" in L.reng_hip_last_error()
     assert L.reng_hip_gemm_w8a16_noalloc(p, p, None, 0, 8, 64, E4M3, p, None) == R.EINVAL
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 3584, 3584), (256, 2048, 8192)])   # K-split partials; stream-K
+def test_noalloc_under_graph_capture_on_a_fresh_stream(R, M, N, K):
+    """What the entry point is for: captured into a hipGraph on a stream that has
+    never run a split-K or stream-K product (so the allocating entry would have
+    to grow its per-stream buffers, which it refuses while the stream is
+    captured), replayed three times with eager work and synchronizations in
+    between; every replay equals the allocating entry's eager result."""
+    rng = np.random.default_rng(M + N + K)
+    x, codes, scales = operands(rng, M, N, K, E4M3)
+    want = call(R, "reng_hip_gemm_w8a16", x, codes, scales, M, N, K, E4M3)
+    torch.cuda.synchronize()
+    L = R.lib()
+    args = lambda y: (ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(codes.data_ptr()),
+                      ctypes.c_void_p(scales.data_ptr()), M, N, K, E4M3, ctypes.c_void_p(y.data_ptr()))
+
+    # The allocating entry on a fresh stream under capture: refused, nothing queued.
+    side = torch.cuda.Stream()
+    y0 = torch.full((M * N,), -1, dtype=torch.int16, device="cuda")
+    g0 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g0, stream=side):
+        rc = L.reng_hip_gemm_w8a16(*args(y0), ctypes.c_void_p(side.cuda_stream))
+    assert rc == R.EINVAL and b"captured" in L.reng_hip_last_error()
+
+    fresh = torch.cuda.Stream()
+    y = torch.full((M * N,), -1, dtype=torch.int16, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=fresh):
+        rc = L.reng_hip_gemm_w8a16_noalloc(*args(y), ctypes.c_void_p(fresh.cuda_stream))
+    assert rc == 0, L.reng_hip_last_error()
+    for rep in range(3):
+        y.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), (M, N, K, rep)
