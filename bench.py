@@ -281,6 +281,14 @@ def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3", read_yardstick=False):
     rec = {"M": M, "N": N, "K": K, "us": round(secs * 1e6, 2), "GBps": round(nbytes / secs / 1e9, 1),
            "hbm_frac": round(ceil.fraction(secs), 3), "bound": ceil.bottleneck.value,
            "TFLOPs": round(flops / secs / 1e12, 2), "rotated_copies": copies}
+    if read_yardstick and 16 < M <= 64 and K % 128 == 0:
+        # The same product's copy stream alone (global -> LDS ring, codes and
+        # activation, no arithmetic): the floor its data movement sets.
+        sink1 = torch.zeros(1, dtype=torch.int32, device="cuda")
+        csecs = graph_time(torch, lambda i: R.stream_stage(x, ws[i % copies][0], M, N, K, sink1),
+                           max(2 * copies, 40))
+        rec["copy_yardstick"] = {"us": round(csecs * 1e6, 2), "hbm_frac": round(ceil.fraction(csecs), 3),
+                                 "kernel_over_copy": round(secs / csecs, 3)}
     if read_yardstick and (N * K) % 1024 == 0:
         # A plain read of the same code bytes, rotated the same way: the
         # fastest one launch of this size reads on this device.
@@ -290,6 +298,16 @@ def bench_w8a16(torch, R, gen, M, N, K, fmt="e4m3", read_yardstick=False):
                                  "hbm_frac": round(N * K / rsecs / HBM_PEAK, 3),
                                  "kernel_over_read": round(secs / rsecs, 3)}
     return rec
+
+
+def launch_floor(torch, R):
+    """The cost of a launch that does (almost) nothing, as these replays see
+    it: the read yardstick over 64 KB (its full grid of 8 blocks per CU) from a
+    hipGraph. Every timed kernel here pays about this much per launch."""
+    bufs = [torch.zeros(64 << 10, dtype=torch.uint8, device="cuda") for _ in range(4)]
+    sink = torch.empty(R.stream_read_sink_bytes(), dtype=torch.uint8, device="cuda")
+    secs = graph_time(torch, lambda i: R.stream_read(bufs[i % 4], 64 << 10, sink), 40)
+    return {"us": round(secs * 1e6, 2), "what": "stream_read over 64 KB, 40 launches replayed from a hipGraph"}
 
 
 def bench_w8a16_tiles(torch, R, gen):
@@ -714,7 +732,8 @@ def main():
         gen.manual_seed(99)
         if args.part == "gemv":
             out = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
-                   bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True)]
+                   bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True),
+                   {"launch_floor": launch_floor(torch, R)}]
         elif args.part == "qwen32b":
             out = [bench_qwen32b_quantize(torch, R, args.format, parity=not args.no_cpu)]
         elif args.part == "host":
@@ -786,7 +805,8 @@ def main():
         extras["f32_2048x2048_quantize"] = bench_f32_quantize(torch, R, gen, cpu=not args.no_cpu)
         extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
                                      bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True)]
-        log("gemv b1:", extras["gemv_b1_llama8b"])
+        extras["launch_floor"] = launch_floor(torch, R)
+        log("gemv b1:", extras["gemv_b1_llama8b"], "launch floor:", extras["launch_floor"])
         sk = []
         for M in (8, 64):
             for _, N, K in QWEN_7B:

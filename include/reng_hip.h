@@ -336,6 +336,16 @@ RENG_HIP_API int reng_hip_stream_read(const void *p, size_t bytes, void *sink, v
  * reference: it exists to measure the memory system. Asynchronous. */
 RENG_HIP_API int reng_hip_stream_narrow(const void *src, size_t elems, void *dst, void *stream);
 
+/* The copy yardstick the 16 < M <= 64 skinny GEMM is measured against: the
+ * data movement of that product's kernel and nothing else - the same grid,
+ * LDS ring, global -> LDS copies of the codes [N, K] and the activation
+ * x [M, K] (bf16), waits and barriers, with no decode, MFMA or output. x and
+ * codes 16-byte aligned, K a positive multiple of 128, 16 < M <= 64; sink is
+ * one device word written only by chance. No counterpart in the reference: it
+ * exists to measure the kernel's copy floor. Asynchronous. */
+RENG_HIP_API int reng_hip_stream_stage(const uint16_t *x, const uint8_t *codes, size_t M, size_t N, size_t K,
+                                       void *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -296,6 +296,19 @@ RENG_HIP_API int reng_hip_stream_narrow(const void *src, size_t elems, void *dst
     return launch_stream_narrow(src, elems, dst, as_stream(stream));
 }
 
+RENG_HIP_API int reng_hip_stream_stage(const uint16_t *x, const uint8_t *codes, size_t M, size_t N, size_t K,
+                                       void *sink, void *stream) {
+    clear_error();
+    RENG_REQUIRE(x && codes && sink, "null pointer");
+    RENG_REQUIRE(M > 16 && M <= 64, "M = %zu outside 17..64", M);
+    RENG_REQUIRE(N > 0 && N <= 0xffffffffu, "N = %zu out of range", N);
+    RENG_REQUIRE(K >= 128 && K % 128 == 0 && K <= 0xffffffffu, "K = %zu is not a positive multiple of 128", K);
+    RENG_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(codes)) & 15) == 0,
+                 "x and codes must be 16-byte aligned");
+    return launch_stage_copy(x, codes, (uint32_t)M, (uint32_t)N, (uint32_t)K, static_cast<uint32_t *>(sink),
+                             as_stream(stream));
+}
+
 RENG_HIP_API int reng_hip_gemm_w8a16_noalloc(const uint16_t *x, const uint8_t *codes, const float *scales,
                                              size_t M, size_t N, size_t K, int format, uint16_t *y,
                                              void *stream) {

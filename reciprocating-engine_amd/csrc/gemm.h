@@ -66,6 +66,10 @@ float *split_partials(size_t floats, hipStream_t st, const SplitScratch *fixed, 
 // holds stream_read_sink_words() words (written only by chance).
 int launch_stream_read(const void *p, size_t bytes, uint32_t *sink, hipStream_t st);
 uint32_t stream_read_sink_words();
+// The stage-copy yardstick: skinny_wide's copy stream (16 < M <= 64,
+// K % 128 == 0) on its own grid with no arithmetic; sink holds one word.
+int launch_stage_copy(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K, uint32_t *sink,
+                      hipStream_t st);
 int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, const uint8_t *b,
                     int fb, const float *sb, uint32_t nsb, uint32_t M, uint32_t N, uint32_t K,
                     uint16_t *out, hipStream_t st);

@@ -68,6 +68,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void copy16(const uint8_t *g, uint8_t *l) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
 }
+// The same for code bytes, which every block reads once: the non-temporal
+// policy (nt) keeps them from displacing the activation the blocks share in
+// L2 (the copy stream alone on Qwen2.5-7B M = 64: [18944, 3584] 18.2 -> 17.6 us,
+// [3584, 18944] 15.4 -> 14.1 us).
+__device__ __forceinline__ void copy16_nt(const uint8_t *g, uint8_t *l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 2);
+}
 
 // s_waitcnt lgkmcnt(0): this wave's LDS reads have returned, so copies may
 // overwrite the slot they read.
@@ -168,7 +175,7 @@ __global__ __launch_bounds__(64 * KW * NW) void skinny_rows(const uint16_t *__re
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t back = (half && ((whi >> (4 * t + i)) & 1)) ? CHUNK : 0u;
-                copy16(wsrc[t][i] + (size_t)st * STAGE_K - back, slot + t * TILE + i * 1024);
+                copy16_nt(wsrc[t][i] + (size_t)st * STAGE_K - back, slot + t * TILE + i * 1024);
             }
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
@@ -414,7 +421,10 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
     auto copies = [&](uint32_t st) {
         uint8_t *slot = lds + (st % S) * SLOT;
 #pragma unroll
-        for (int c = 0; c < C; ++c) copy16(src[c] + (size_t)st * BK * unit[c], slot + dst[c]);
+        for (int c = 0; c < C; ++c) {
+            if (unit[c] == 1) copy16_nt(src[c] + (size_t)st * BK, slot + dst[c]);
+            else copy16(src[c] + (size_t)st * BK * 2, slot + dst[c]);
+        }
     };
 
     f32x4 acc[NTW][MTW];
@@ -524,6 +534,73 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
     }
 }
 
+// The copy stream of skinny_wide and nothing else, a yardstick for bench.py:
+// the same grid, block, S-slot LDS ring, copies (codes R / 8 x 1 KB and
+// activation 16 MT rows per stage, by global_load_lds), waits and barriers,
+// with no fragment reads, decodes, MFMAs or output. Its time is the floor that
+// the kernel's data movement alone sets. sink gets one word if a (never
+// matching) value turns up, which keeps the copies live.
+template <int MT, int NTW, int S>
+__global__ __launch_bounds__(256) void stage_copy_kernel(const uint16_t *__restrict__ x,
+                                                         const uint8_t *__restrict__ codes, uint32_t M, uint32_t N,
+                                                         uint32_t K, uint32_t cps, uint32_t *sink) {
+    constexpr int BK = CHUNK, R = 32 * NTW, AR = 16 * MT;
+    constexpr int WB = R * BK, AB = AR * BK * 2, SLOT = WB + AB;
+    constexpr int WC = R / 8, AC = AR / 4;
+    constexpr int C = (WC + AC) / 4;
+    static_assert(WC % 4 == 0 && AC % 4 == 0 && S >= 2 && (S - 2) * C < 64, "as skinny_wide");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * SLOT];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t n0 = blockIdx.x * R;
+    const uint32_t chunks = K / CHUNK;
+    const uint32_t kc0 = blockIdx.y * cps, kc1 = kc0 + cps < chunks ? kc0 + cps : chunks;
+    const uint32_t nst = kc1 - kc0;
+    const uint8_t *src[C];
+    uint32_t dst[C], unit[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int q = wave + 4 * c;
+        if (q < WC) {
+            const uint32_t rr = q * 8 + lane / 8, p = (lane % 8) ^ swz8(rr);
+            uint32_t n = n0 + rr;
+            n = n < N ? n : N - 1;
+            src[c] = codes + (size_t)n * K + (size_t)kc0 * CHUNK + p * 16;
+            dst[c] = q * 1024;
+            unit[c] = 1;
+        } else {
+            const int qa = q - WC;
+            const uint32_t row = qa * 4 + lane / 16, p = (lane % 16) ^ (row & 15);
+            const uint32_t m = row < M ? row : M - 1;
+            src[c] = reinterpret_cast<const uint8_t *>(x + (size_t)m * K + (size_t)kc0 * CHUNK + p * 8);
+            dst[c] = WB + qa * 1024;
+            unit[c] = 2;
+        }
+    }
+    auto copies = [&](uint32_t st) {
+        uint8_t *slot = lds + (st % S) * SLOT;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            if (unit[c] == 1) copy16_nt(src[c] + (size_t)st * BK, slot + dst[c]);
+            else copy16(src[c] + (size_t)st * BK * 2, slot + dst[c]);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if ((uint32_t)s < nst) copies(s);
+    for (uint32_t st = 0; st < nst; ++st) {
+        if (st + S - 2 < nst) wait_vmcnt<(S - 2) * C>();
+        else wait_vmcnt<0>();
+        wait_lgkm0();
+        lds_barrier();
+        if (st + S - 1 < nst) copies(st + S - 1);
+    }
+    wait_vmcnt<0>();
+    lds_barrier();
+    const uint32_t v = reinterpret_cast<const uint32_t *>(lds)[tid];
+    if (v == 0x9e3779b9u) sink[0] = v;
+}
+
 // y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the splits added in order; four
 // consecutive n per thread when N % 4 == 0 (16-byte reads, 8-byte stores).
 // The loads of the first 16 splits are issued together (one memory round
@@ -629,6 +706,32 @@ int launch_wide_mt(const uint16_t *x, const uint8_t *codes, const float *scales,
     return launch_wide_cfg<F, MT, 4, 3>(x, codes, scales, M, N, K, y, st, fixed);
 }
 
+// The stage-copy yardstick on the grid skinny_wide would take for this product.
+template <int MT, int NTW, int S>
+int launch_stage_copy_cfg(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K,
+                          uint32_t *sink, hipStream_t st) {
+    const uint32_t tiles = (N + 32 * NTW - 1) / (32 * NTW);
+    const uint32_t chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
+    const uint32_t max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
+    uint32_t splits = cus / tiles;
+    splits = splits < 1 ? 1 : splits > max_splits ? max_splits : splits;
+    const uint32_t cps = (chunks + splits - 1) / splits;
+    splits = (chunks + cps - 1) / cps;
+    hipLaunchKernelGGL((stage_copy_kernel<MT, NTW, S>), dim3(tiles, splits), dim3(256), 0, st, x, codes, M, N, K, cps,
+                       sink);
+    return check_launch("stage_copy");
+}
+
+template <int MT>
+int launch_stage_copy_mt(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K,
+                         uint32_t *sink, hipStream_t st) {
+    if ((uint64_t)N * K <= (16ull << 20)) return launch_stage_copy_cfg<MT, 2, 4>(x, codes, M, N, K, sink, st);
+    const uint32_t cus = (uint32_t)device_props().cus, b128 = wide_blocks(N, K, 128);
+    if (10 * b128 < 7 * cus && wide_blocks(N, K, 96) > b128)
+        return launch_stage_copy_cfg<MT, 3, 4>(x, codes, M, N, K, sink, st);
+    return launch_stage_copy_cfg<MT, 4, 3>(x, codes, M, N, K, sink, st);
+}
+
 template <int F>
 int launch_wide_f(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                   uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
@@ -640,6 +743,17 @@ int launch_wide_f(const uint16_t *x, const uint8_t *codes, const float *scales, 
 }
 
 }  // namespace skinny
+
+// 16 < M <= 64, K % 128 == 0: skinny_wide's copy stream alone (a yardstick).
+int launch_stage_copy(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K, uint32_t *sink,
+                      hipStream_t st) {
+    using namespace skinny;
+    switch ((M + 15) / 16) {
+        case 2: return launch_stage_copy_mt<2>(x, codes, M, N, K, sink, st);
+        case 3: return launch_stage_copy_mt<3>(x, codes, M, N, K, sink, st);
+        default: return launch_stage_copy_mt<4>(x, codes, M, N, K, sink, st);
+    }
+}
 
 // 2 <= M <= 16, K % 128 == 0 (rows past M repeat row M - 1 and are not stored).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,

@@ -77,6 +77,7 @@ SIGNATURES = {
     "reng_hip_stream_read_sink_bytes": (_SZ, []),
     "reng_hip_stream_read": (_I, [_P, _SZ, _P, _P]),
     "reng_hip_stream_narrow": (_I, [_P, _SZ, _P, _P]),
+    "reng_hip_stream_stage": (_I, [_P, _P, _SZ, _SZ, _SZ, _P, _P]),
 }
 
 
@@ -537,6 +538,14 @@ def stream_narrow(src, elems, dst):
     """The stream yardstick: the high byte of each of elems bf16 values of src
     into dst (device tensors)."""
     _check(lib().reng_hip_stream_narrow(_dev(src, "src", 2 * elems), elems, _dev(dst, "dst", elems), _stream()))
+
+
+def stream_stage(x, codes, M, N, K, sink):
+    """The copy yardstick of the 16 < M <= 64 skinny GEMM: its global -> LDS
+    copy stream for x [M, K] and codes [N, K] with no arithmetic (device tensors;
+    sink: a device tensor of at least 4 bytes)."""
+    _check(lib().reng_hip_stream_stage(_dev(x, "x", 2 * M * K), _dev(codes, "codes", N * K), M, N, K,
+                                       _dev(sink, "sink", 4), _stream()))
 
 
 def stream_read_sink_bytes():

@@ -73,7 +73,13 @@ def test_refusals_happen_before_any_device_work():
     arr = (R._Matrix * 1)()
     rc = L.reng_hip_quantize_batch(arr, 0, R.BF16, R.E4M3, R.PCS, 1.0, None)
     assert rc == R.EINVAL
-    # The two yardsticks bench.py measures with.
+    # The three yardsticks bench.py measures with.
+    rc = L.reng_hip_stream_stage(p, p, 16, 512, 3584, p, None)
+    assert rc == R.EINVAL and b"outside 17..64" in L.reng_hip_last_error()
+    rc = L.reng_hip_stream_stage(p, p, 64, 512, 3600, p, None)
+    assert rc == R.EINVAL and b"multiple of 128" in L.reng_hip_last_error()
+    rc = L.reng_hip_stream_stage(ctypes.c_void_p(8), p, 64, 512, 3584, p, None)
+    assert rc == R.EINVAL and b"16-byte aligned" in L.reng_hip_last_error()
     rc = L.reng_hip_stream_read(p, 1000, p, None)
     assert rc == R.EINVAL and b"multiple of 1024" in L.reng_hip_last_error()
     rc = L.reng_hip_stream_narrow(p, 12, p, None)

@@ -418,3 +418,16 @@ def test_fp8_gemm_every_output_of_the_qwen_32b_long_shapes(R, shape):
                                      M, N, K)).reshape(M, N)
     assert np.all(np.isfinite(out))
     assert_elementwise(out, qa.dequantize(), qw.dequantize(), K, f"M={M} N={N} K={K}", acc=fp8_acc(K))
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 512, 3584), (40, 3584, 3584), (64, 18944, 3584), (64, 3584, 18944)])
+def test_the_stage_copy_yardstick_runs_the_skinny_grid(R, M, N, K):
+    """reng_hip_stream_stage (skinny_wide's copy stream with no arithmetic, a
+    measuring stick for bench.py) on each block shape the wide kernel takes:
+    it completes, and with all-zero operands never writes its sink."""
+    x = torch.zeros(M * K, dtype=torch.int16, device="cuda")
+    c = torch.zeros(N * K, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    R.stream_stage(x, c, M, N, K, sink)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
