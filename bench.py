@@ -310,6 +310,30 @@ def launch_floor(torch, R):
     return {"us": round(secs * 1e6, 2), "what": "stream_read over 64 KB, 40 launches replayed from a hipGraph"}
 
 
+def read_fit(torch, R, sizes_mb=(8, 16, 32, 64, 128, 256)):
+    """The read yardstick's launch time over sizes, fitted as a fixed part plus
+    bytes over a streaming rate (least squares). The fixed part is what any one
+    launch of these sizes pays on top of its bytes; the rate is what a plain
+    read sustains once it streams."""
+    sink = torch.empty(R.stream_read_sink_bytes(), dtype=torch.uint8, device="cuda")
+    pts = []
+    for mb in sizes_mb:
+        n = mb << 20
+        copies = rotation(n)
+        bufs = [torch.zeros(n, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        secs = graph_time(torch, lambda i: R.stream_read(bufs[i % copies], n, sink), max(2 * copies, 40))
+        pts.append((n, secs))
+        del bufs
+    k = len(pts)
+    sx = sum(p[0] for p in pts); sy = sum(p[1] for p in pts)
+    sxx = sum(p[0] * p[0] for p in pts); sxy = sum(p[0] * p[1] for p in pts)
+    slope = (k * sxy - sx * sy) / (k * sxx - sx * sx)
+    icpt = (sy - slope * sx) / k
+    return {"fixed_us": round(icpt * 1e6, 2), "stream_TBps": round(1e-12 / slope, 2),
+            "points": [{"MB": n >> 20, "us": round(s * 1e6, 2)} for n, s in pts],
+            "what": "stream_read over rotated buffers, t = fixed + bytes / rate"}
+
+
 def bench_w8a16_tiles(torch, R, gen):
     """More than 64 activation rows (the tiled bf16-MFMA kernel): M = 256 on the
     reference probe's timed shapes (fp8_probe.rs:359-431), the Llama-3.1-8B
@@ -733,7 +757,7 @@ def main():
         if args.part == "gemv":
             out = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
                    bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True),
-                   {"launch_floor": launch_floor(torch, R)}]
+                   {"launch_floor": launch_floor(torch, R)}, {"read_fit": read_fit(torch, R)}]
         elif args.part == "qwen32b":
             out = [bench_qwen32b_quantize(torch, R, args.format, parity=not args.no_cpu)]
         elif args.part == "host":
@@ -806,7 +830,9 @@ def main():
         extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
                                      bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True)]
         extras["launch_floor"] = launch_floor(torch, R)
-        log("gemv b1:", extras["gemv_b1_llama8b"], "launch floor:", extras["launch_floor"])
+        extras["read_fit"] = read_fit(torch, R)
+        log("gemv b1:", extras["gemv_b1_llama8b"], "launch floor:", extras["launch_floor"],
+            "read fit:", extras["read_fit"])
         sk = []
         for M in (8, 64):
             for _, N, K in QWEN_7B:
