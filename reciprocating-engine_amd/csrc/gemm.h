@@ -37,9 +37,9 @@ int launch_gemv_norm(const float *x, const float *gamma, float eps, const uint8_
 int launch_gemv_norm_rope(const float *x, const float *gamma, float eps, const uint8_t *codes, const float *scales,
                           uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t K, int format, const float *sin_row,
                           const float *cos_row, uint16_t *q, uint16_t *k_row, uint16_t *v_row, hipStream_t st);
-// 4 < M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
+// 2 <= M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                       uint32_t K, int format, uint16_t *y, hipStream_t st);
+                       uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed);
 // 16 < M <= 64 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed);

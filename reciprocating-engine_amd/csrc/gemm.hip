@@ -847,7 +847,7 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     // GEMV's per-row dot products (Qwen2.5-7B [3584, 18944]: M = 3 26.3 ->
     // 16.6 us, M = 2 22.5 -> 16.6 us; M = 2 with a short K stays on the GEMV).
     if (M >= 2 && M <= 4 && K % 128 == 0 && (M >= 3 || (size_t)M * K * 2 > 64 * 1024))
-        return launch_skinny_mfma(x, codes, scales, M, N, K, F, y, st);
+        return launch_skinny_mfma(x, codes, scales, M, N, K, F, y, st, fixed);
     if (M <= 4) {
         const GemvPlan p = gemv_plan(M, N, K, 1);
         const uint32_t blocks = p.blocks;
@@ -877,7 +877,8 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     // Larger M: tiles of up to 64 activation rows on the MFMA kernels.
     for (uint32_t mb = 0; mb < M; mb += 64) {
         const uint32_t mt = M - mb < 64 ? M - mb : 64;
-        const int rc = mt <= 16 ? launch_skinny_mfma(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st)
+        const int rc = mt <= 16 ? launch_skinny_mfma(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st,
+                                                     fixed)
                                 : launch_skinny_wide(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st,
                                                      fixed);
         if (rc) return rc;

@@ -11,10 +11,15 @@
 // instruction: that pattern streams HBM at ~4 TB/s on this device against
 // ~5.5 TB/s for 4 rows x 256 bytes. So the codes (and the activation) go
 // through LDS: copied in 4 x 256-byte pieces by global_load_lds and read back
-// transposed (skinny_rows for M <= 16: one launch, no partial sums in memory;
-// skinny_wide for 16 < M <= 64, where a block must cover many weight rows per
-// activation byte it reads and so splits K over blocks).
+// transposed (skinny_rows for M <= 16: whole-K blocks, no partial sums in
+// memory; skinny_wide for 16 < M <= 64, where a block must cover many weight
+// rows per activation byte it reads, and for the M <= 16 products skinny_rows
+// runs on too few blocks: it splits K over blocks and merges the splits'
+// partial sums inside the same launch).
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "common.h"
 #include "gemm.h"
@@ -359,41 +364,135 @@ int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint
 }
 
 
-// 16 < M <= 64. The activation is 128 bytes per k at M = 64 against R bytes
-// of codes for R weight rows, so a block covers R = 32 NTW rows (64 or 128)
-// and shares one copy of each stage between its 4 waves: stages of BK = 128
-// codes in an S-slot LDS ring (one barrier per stage), filled by global_load_lds
+// Up to 64 activation rows over many weight rows per activation byte. At
+// M = 64 the activation is 128 bytes per k against R bytes of codes for R
+// weight rows, so a block covers R = 32 NTW rows (32 to 128) and shares one
+// copy of each stage between its 4 waves: stages of BK = 128 codes in an
+// S-slot LDS ring (one barrier per stage), filled by global_load_lds
 //   codes: R / 8 copies of 8 rows x 128 bytes, piece p of row r in slot p ^ swz8(r);
 //   activation: 16 MT rows (>= M repeat row M - 1), 4 rows x 256 bytes per copy,
 //     8-element piece p of row r in slot p ^ (r % 16);
-// spread over the waves. Wave (wn, wm) computes rows [wn R / 2, +R / 2) against
-// activation tiles wm, wm + 2 (< MT). Blocks split K (blockIdx.y takes chunks
-// [y cps, +cps)) until the grid fills the CUs; with more than one split the
-// partial products go to part[y][m][n] (f32, 16-byte stores) and
-// reduce_splits adds them in split order.
+// spread over the waves. The waves form a WNC x WMC grid (2 x 2 for MT >= 2,
+// 4 x 1 for MT = 1): wave (wn, wm) computes rows [wn R / WNC, +R / WNC)
+// against activation tiles wm, wm + WMC, ... (< MT).
+//
+// Blocks split K until the grid fills the CUs (split s takes chunks
+// [s cps, +cps)). The splits of a row tile meet inside the launch: each block
+// writes its f32 fragments to the tile's slot for its split, counts itself in
+// on cnt[tile], and the last block of the tile to count in reads every split's
+// fragments, adds them in split order (the same order whichever block is
+// last, so the sums are deterministic), applies the scales, writes the tile
+// and resets the counter for the next launch. No block waits for another.
+// With splits, the grid is XCD-major: block b runs on XCD b % 8 (workgroups
+// are dealt to the 8 XCDs round-robin) and takes tile (b / 8 / splits) * 8 +
+// b % 8, so a tile's splits share one XCD's L2, where the partials go with
+// plain stores and come back with L1-bypassing (sc0) loads. If the device was
+// not seen to place workgroups that way (xcd_placement), the partials go
+// through agent-coherent (sc1) stores and loads instead.
 __device__ __forceinline__ uint32_t swz8(uint32_t r) { return (r ^ ((r >> 3) & 1)) & 7; }
+
+// The tile's last block learns it here; its frag then hold the sums over the
+// splits. Slot (tile, split) holds waves x NF x 64 f32x4, fragment f of lane l
+// of wave w at (w NF + f) 64 + l. Every block of the tile calls this (it has
+// barriers). part is addressed through a buffer resource of part_bytes, so
+// the loads of a group past the last split fetch nothing.
+template <int NF>
+__device__ __forceinline__ bool merge_splits(f32x4 (&frag)[NF], float *part, uint32_t part_bytes, uint32_t *cnt,
+                                             uint32_t tile, uint32_t split, uint32_t splits, uint32_t coh,
+                                             uint32_t *flag) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, 0, part_bytes, 0x00020000);
+    const uint32_t slot = (uint32_t)waves * NF * 64 * 16;   // bytes per (tile, split)
+    const uint32_t lo = (uint32_t)(wave * NF * 64 + lane) * 16;
+    const uint32_t mine = (tile * splits + split) * slot + lo;
+    if (coh) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, frag[f]), rs, mine + f * 1024, 0, 16);
+    } else {
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, frag[f]), rs, mine + f * 1024, 0, 0);
+    }
+    asm volatile("" ::: "memory");
+    wait_vmcnt<0>();   // this wave's fragments are in the cache the last block reads
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t seen = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = seen + 1 == splits;
+    }
+    __syncthreads();
+    if (!*flag) return false;
+    asm volatile("" ::: "memory");
+    // Eight splits' fragments requested together, then added in order.
+    const uint32_t base = tile * splits * slot + lo;
+    constexpr uint32_t PAST = 0xf8000000u;   // past any part_bytes (<= 0xf0000000): loads nothing
+    for (uint32_t s0 = 0; s0 < splits; s0 += 8) {
+        u32x4 v[8][NF];
+        if (coh) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t off = s0 + i < splits ? base + (s0 + i) * slot : PAST;
+#pragma unroll
+                for (int f = 0; f < NF; ++f) v[i][f] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + f * 1024, 0, 16);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t off = s0 + i < splits ? base + (s0 + i) * slot : PAST;
+#pragma unroll
+                for (int f = 0; f < NF; ++f) v[i][f] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + f * 1024, 0, 1);
+            }
+        }
+        asm volatile("" ::: "memory");   // all of the group's loads before the first add
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const bool ok = s0 + i < splits, first = s0 + i == 0;
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const f32x4 x = __builtin_bit_cast(f32x4, v[i][f]);
+                const f32x4 n = first ? x : frag[f] + x;
+                frag[f] = ok ? n : frag[f];
+            }
+        }
+    }
+    if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
 
 template <int F, int MT, int NTW, int S>
 __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes,
                                                    const float *__restrict__ scales, uint32_t M, uint32_t N,
-                                                   uint32_t K, uint32_t cps, uint16_t *__restrict__ y,
-                                                   float *__restrict__ part) {
+                                                   uint32_t K, uint32_t tiles, uint32_t splits, uint32_t cps,
+                                                   uint16_t *__restrict__ y, float *part, uint32_t part_bytes,
+                                                   uint32_t *cnt, uint32_t coh) {
     constexpr int BK = CHUNK, R = 32 * NTW, AR = 16 * MT;
     constexpr int WB = R * BK, AB = AR * BK * 2, SLOT = WB + AB;
     constexpr int WC = R / 8, AC = AR / 4;          // copies per stage (block)
     static_assert(WC % 4 == 0 && AC % 4 == 0, "copies split evenly over 4 waves");
     constexpr int C = (WC + AC) / 4;                // copies per stage per wave
     static_assert(S >= 2 && (S - 2) * C < 64, "vmcnt");
-    constexpr int MTW = (MT + 1) / 2;               // activation tiles per wave
+    constexpr int WMC = MT >= 2 ? 2 : 1, WNC = 4 / WMC;
+    constexpr int TPW = R / (16 * WNC);             // 16-row tiles per wave
+    static_assert(TPW >= 1 && TPW * 16 * WNC == R, "rows split evenly over the wave rows");
+    constexpr int MTW = (MT + WMC - 1) / WMC;       // activation tiles per wave
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * SLOT];
+    __shared__ uint32_t last_flag;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave >> 1, wm = wave & 1;
+    const int wn = wave / WMC, wm = wave % WMC;
     const uint32_t r16 = lane & 15, g = lane >> 4;
-    const uint32_t n0 = blockIdx.x * R;
+    uint32_t tile = blockIdx.x, split = 0;
+    if (splits > 1) {
+        const uint32_t j = blockIdx.x / 8;
+        tile = (j / splits) * 8 + blockIdx.x % 8;
+        split = j % splits;
+        if (tile >= tiles) return;   // the XCD-major grid's padding
+    }
+    const uint32_t n0 = tile * R;
     const uint32_t chunks = K / CHUNK;
-    const uint32_t kc0 = blockIdx.y * cps, kc1 = kc0 + cps < chunks ? kc0 + cps : chunks;
+    const uint32_t kc0 = split * cps, kc1 = kc0 + cps < chunks ? kc0 + cps : chunks;
     const uint32_t nst = kc1 - kc0;
 
     // This wave's copies q = wave + 4 c: q < WC a code copy, else activation copy q - WC.
@@ -427,18 +526,16 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
         }
     };
 
-    f32x4 acc[NTW][MTW];
+    f32x4 acc[TPW * MTW];   // fragment (t, u) at t MTW + u
 #pragma unroll
-    for (int t = 0; t < NTW; ++t)
-#pragma unroll
-        for (int u = 0; u < MTW; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < TPW * MTW; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     auto compute = [&](uint32_t st) {
         const uint8_t *slot = lds + (st % S) * SLOT;
-        u32x4 w[NTW][2];
+        u32x4 w[TPW][2];
 #pragma unroll
-        for (int t = 0; t < NTW; ++t) {
-            const uint32_t rr = wn * (R / 2) + t * 16 + r16;
+        for (int t = 0; t < TPW; ++t) {
+            const uint32_t rr = wn * (R / WNC) + t * 16 + r16;
             const uint8_t *rb = slot + rr * BK;
             w[t][0] = *reinterpret_cast<const u32x4 *>(rb + ((g ^ swz8(rr)) * 16));
             w[t][1] = *reinterpret_cast<const u32x4 *>(rb + (((4 + g) ^ swz8(rr)) * 16));
@@ -446,7 +543,7 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
         u32x4 a[MTW][4];
 #pragma unroll
         for (int u = 0; u < MTW; ++u) {
-            const int mt = wm + 2 * u;
+            const int mt = wm + WMC * u;
             uint32_t am = (mt < MT ? mt : MT - 1) * 16 + r16;
             am = am < M ? am : M - 1;
             const uint8_t *arow = slot + WB + am * (BK * 2);
@@ -459,28 +556,28 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
-            for (int t = 0; t < NTW; ++t) {
+            for (int t = 0; t < TPW; ++t) {
                 const u32x4 &q = w[t][j >> 1];
                 const bf16x8 wa = (j & 1) ? dec8<F>(q.z, q.w) : dec8<F>(q.x, q.y);
 #pragma unroll
                 for (int u = 0; u < MTW; ++u) {
-                    if (wm + 2 * u >= MT) break;
-                    acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, __builtin_bit_cast(bf16x8, a[u][j]),
-                                                                       acc[t][u], 0, 0, 0);
+                    if (wm + WMC * u >= MT) break;
+                    acc[t * MTW + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        wa, __builtin_bit_cast(bf16x8, a[u][j]), acc[t * MTW + u], 0, 0, 0);
                 }
             }
         }
     };
 
-    // Without K splits this block applies the scales: requested before any
-    // copy (older than everything the explicit waits count).
-    float sc[NTW][4];
+    // The scales of this lane's output rows, requested before any copy (older
+    // than everything the explicit waits count; used after the loop).
+    float sc[TPW][4];
 #pragma unroll
-    for (int t = 0; t < NTW; ++t)
+    for (int t = 0; t < TPW; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t n = n0 + wn * (R / 2) + t * 16 + 4 * g + e;
-            sc[t][e] = (scales && !part) ? scales[n < N ? n : N - 1] : 1.0f;
+            const uint32_t n = n0 + wn * (R / WNC) + t * 16 + 4 * g + e;
+            sc[t][e] = scales ? scales[n < N ? n : N - 1] : 1.0f;
         }
 
 #pragma unroll
@@ -495,40 +592,32 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
         compute(st);
     }
 
+    if (splits > 1 && !merge_splits<TPW * MTW>(acc, part, part_bytes, cnt, tile, split, splits, coh, &last_flag))
+        return;
+
     // Lane holds column m = 16 mt + l % 16 and rows n = 4 (l / 16) + e.
 #pragma unroll
     for (int u = 0; u < MTW; ++u) {
-        const int mt = wm + 2 * u;
+        const int mt = wm + WMC * u;
         if (mt >= MT) break;
         const uint32_t m = mt * 16 + r16;
         if (m >= M) continue;
 #pragma unroll
-        for (int t = 0; t < NTW; ++t) {
-            const uint32_t nb = n0 + wn * (R / 2) + t * 16 + 4 * g;
-            const f32x4 s = acc[t][u];
-            if (part) {
-                float *pp = part + ((size_t)blockIdx.y * M + m) * N;
-                if (nb + 3 < N && (N & 3) == 0) {
-                    *reinterpret_cast<f32x4 *>(pp + nb) = s;
-                } else {
+        for (int t = 0; t < TPW; ++t) {
+            const uint32_t nb = n0 + wn * (R / WNC) + t * 16 + 4 * g;
+            const f32x4 s = acc[t * MTW + u];
+            float o[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (nb + e < N) pp[nb + e] = s[e];
-                }
+            for (int e = 0; e < 4; ++e) o[e] = s[e] * sc[t][e];
+            uint16_t *yr = y + (size_t)m * N;
+            if (nb + 3 < N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+                *reinterpret_cast<u32x2 *>(yr + nb) =
+                    u32x2{f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16),
+                          f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16)};
             } else {
-                float o[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = s[e] * sc[t][e];
-                uint16_t *yr = y + (size_t)m * N;
-                if (nb + 3 < N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
-                    *reinterpret_cast<u32x2 *>(yr + nb) =
-                        u32x2{f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16),
-                              f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16)};
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (nb + e < N) yr[nb + e] = (uint16_t)f32_to_bf16_bits(o[e]);
-                }
+                for (int e = 0; e < 4; ++e)
+                    if (nb + e < N) yr[nb + e] = (uint16_t)f32_to_bf16_bits(o[e]);
             }
         }
     }
@@ -601,141 +690,171 @@ __global__ __launch_bounds__(256) void stage_copy_kernel(const uint16_t *__restr
     if (v == 0x9e3779b9u) sink[0] = v;
 }
 
-// y[m, n] = bf16(s[n] * sum_k part[k][m][n]), the splits added in order; four
-// consecutive n per thread when N % 4 == 0 (16-byte reads, 8-byte stores).
-// The loads of the first 16 splits are issued together (one memory round
-// trip for the split counts the launcher makes at these shapes), later ones
-// eight at a time; the splits are added in order.
-__device__ __forceinline__ f32x4 sum_splits4(const float *part, uint32_t splits, uint64_t total, uint64_t i) {
-    const f32x4 *p = reinterpret_cast<const f32x4 *>(part) + i;
-    const uint64_t stride = total / 4;
-    constexpr uint32_t B = 16;
-    f32x4 v[B];
-#pragma unroll
-    for (uint32_t u = 0; u < B; ++u) v[u] = u < splits ? p[u * stride] : f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 a = v[0];
-#pragma unroll
-    for (uint32_t u = 1; u < B; ++u)
-        if (u < splits) a += v[u];
-    for (uint32_t k = B; k < splits; k += 8) {
-        f32x4 w[8];
-#pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) w[u] = k + u < splits ? p[(k + u) * stride] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (uint32_t u = 0; u < 8; ++u)
-            if (k + u < splits) a += w[u];
-    }
-    return a;
+// The XCD of each workgroup of a 1-D grid (hardware register XCC_ID).
+__global__ __launch_bounds__(64) void xcc_probe(uint32_t *out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 0xfu;
 }
 
-__global__ __launch_bounds__(64) void reduce_splits(const float *__restrict__ part, uint32_t splits, uint32_t M,
-                                                    uint32_t N, const float *__restrict__ scales,
-                                                    uint16_t *__restrict__ y) {
-    const uint64_t total = (uint64_t)M * N;
-    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
-    if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
-        for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total / 4; i += step) {
-            const f32x4 a = sum_splits4(part, splits, total, i);
-            const uint32_t n = (uint32_t)((4 * i) % N);
-            const f32x4 sc = scales ? *reinterpret_cast<const f32x4 *>(scales + n) : f32x4{1.f, 1.f, 1.f, 1.f};
-            reinterpret_cast<u32x2 *>(y)[i] =
-                u32x2{f32_to_bf16_bits(a.x * sc.x) | (f32_to_bf16_bits(a.y * sc.y) << 16),
-                      f32_to_bf16_bits(a.z * sc.z) | (f32_to_bf16_bits(a.w * sc.w) << 16)};
-        }
-    } else {
-        for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total; i += step) {
-            float a = part[i];
-            for (uint32_t k = 1; k < splits; ++k) a += part[k * total + i];
-            y[i] = (uint16_t)f32_to_bf16_bits(a * (scales ? scales[i % N] : 1.0f));
-        }
-    }
+// The cache policy of the split merge: 0 (plain stores, sc0 loads) once the
+// device has been seen to run workgroup b on the XCD of workgroup b % 8, as
+// the XCD-major grid needs; 1 (agent-coherent sc1 stores and loads, right
+// wherever blocks run) until then and if it was not. The check runs once per
+// device, over 2048 workgroups, on the caller's stream when a call may
+// allocate and the stream is not being captured. The policy changes where the
+// partials travel, never the sums.
+uint32_t split_coherence(hipStream_t st, bool may_check) {
+    static std::mutex mu;
+    static std::map<int, bool> periodic;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1u;
+    std::lock_guard<std::mutex> lk(mu);
+    const auto it = periodic.find(dev);
+    if (it != periodic.end()) return it->second ? 0u : 1u;
+    if (!may_check) return 1u;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return 1u;
+    constexpr uint32_t G = 2048;
+    uint32_t *d = nullptr;
+    if (hipMalloc(&d, G * sizeof(uint32_t)) != hipSuccess) return 1u;
+    std::vector<uint32_t> h(G, 0xffffffffu);
+    hipLaunchKernelGGL(xcc_probe, dim3(G), dim3(64), 0, st, d);
+    const bool ran = hipGetLastError() == hipSuccess &&
+                     hipMemcpyAsync(h.data(), d, G * sizeof(uint32_t), hipMemcpyDeviceToHost, st) == hipSuccess &&
+                     hipStreamSynchronize(st) == hipSuccess;
+    (void)hipFree(d);
+    if (!ran) return 1u;
+    bool ok = true;
+    for (uint32_t i = 0; i < G; ++i) ok = ok && h[i] < 16 && h[i] == h[i % 8];
+    periodic[dev] = ok;
+    return ok ? 0u : 1u;
 }
 
-// Grid: ceil(N / R) row tiles times K splits, about one block per CU (the
-// ring takes 128-144 KB of LDS).
+// A launch of skinny_wide: R = 32 ntw rows per block, an s-slot ring, the
+// product's row tiles and K splits (cps chunks each).
+struct WidePlan {
+    uint32_t ntw, s, tiles, splits, cps;
+};
+
+// Rows per block first: for 16 < M <= 64 (mt >= 2), 64 on small matrices (the
+// partials of more splits cost more than the activation re-reads) or 32 where
+// 64-row blocks split as far as they go would keep under half the CUs busy
+// (Qwen2.5-7B kv [512, 3584] at M = 64: 8.84 -> 6.94 us); on large ones 128
+// (half the activation bytes per code) unless 128-row blocks leave over 30%
+// of the CUs idle and 96-row ones cover more (Qwen2.5-7B gate/up [18944, 3584]:
+// 148 -> 198 blocks). For M <= 16 (mt = 1, one 16-row activation tile) 64,
+// or 128 on large matrices. Ring depths from sweeps of 3-6 stages on MI355X.
+// Then the splits: as many as keep each XCD's share of the grid (ceil(tiles /
+// 8) row tiles times the splits) within its CUs, so the grid runs in one
+// round, with at least 4 chunks (512 codes) per split.
+WidePlan wide_plan(uint32_t mt, uint32_t N, uint32_t K) {
+    const uint32_t cus = (uint32_t)device_props().cus, per_xcd = cus / 8 > 0 ? cus / 8 : 1;
+    const uint32_t chunks = K / CHUNK, max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
+    auto tiles_of = [&](uint32_t R) { return (N + R - 1) / R; };
+    auto splits_of = [&](uint32_t R) {
+        const uint32_t t = tiles_of(R);
+        if (t >= cus) return 1u;
+        const uint32_t sp = per_xcd / ((t + 7) / 8);
+        return sp < 1 ? 1u : sp > max_splits ? max_splits : sp;
+    };
+    const bool small = (uint64_t)N * K <= (16ull << 20);
+    WidePlan p{2, 4, 0, 1, chunks};
+    if (mt >= 2) {
+        if (small) {
+            if (2 * tiles_of(64) * max_splits < cus) p.ntw = 1;
+        } else {
+            const uint32_t b128 = tiles_of(128) * splits_of(128), b96 = tiles_of(96) * splits_of(96);
+            if (10 * b128 < 7 * cus && b96 > b128) {
+                p.ntw = 3;
+            } else {
+                p.ntw = 4;
+                p.s = 3;
+            }
+        }
+    } else if (!small) {
+        p.ntw = 4;
+    }
+    const uint32_t R = 32 * p.ntw;
+    p.tiles = tiles_of(R);
+    const uint32_t sp = splits_of(R);
+    p.cps = (chunks + sp - 1) / sp;
+    p.splits = (chunks + p.cps - 1) / p.cps;
+    return p;
+}
+
 template <int F, int MT, int NTW, int S>
 int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                    uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
-    const uint32_t tiles = (N + 32 * NTW - 1) / (32 * NTW);
-    const uint32_t chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
-    // At least 4 chunks (512 codes) per split: below that the partials
-    // outweigh the codes.
-    const uint32_t max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
-    uint32_t splits = cus / tiles;
-    splits = splits < 1 ? 1 : splits > max_splits ? max_splits : splits;
-    const uint32_t cps = (chunks + splits - 1) / splits;
-    splits = (chunks + cps - 1) / cps;
-    int rc = RENG_HIP_OK;
-    float *part = splits > 1 ? split_partials((size_t)splits * M * N, st, fixed, &rc) : nullptr;
-    if (rc) return rc;
-    hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S>), dim3(tiles, splits), dim3(256), 0, st, x, codes, scales, M, N,
-                       K, cps, y, part);
-    rc = check_launch("skinny_wide");
-    if (rc || !part) return rc;
-    uint64_t blocks = ((uint64_t)M * N / 4 + 63) / 64;
-    blocks = blocks < 1 ? 1 : blocks > 16ull * cus ? 16ull * cus : blocks;
-    hipLaunchKernelGGL(reduce_splits, dim3((unsigned)blocks), dim3(64), 0, st, part, splits, M, N, scales, y);
-    return check_launch("reduce_splits");
-}
-
-// The (tiles, splits) launch_wide_cfg makes for R-row blocks.
-inline uint32_t wide_blocks(uint32_t N, uint32_t K, uint32_t R) {
-    const uint32_t tiles = (N + R - 1) / R, chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
-    const uint32_t max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
-    uint32_t splits = cus / tiles;
-    splits = splits < 1 ? 1 : splits > max_splits ? max_splits : splits;
-    return tiles * splits;
+                    uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed, const WidePlan &p) {
+    constexpr uint32_t WMC = MT >= 2 ? 2 : 1, TPW = 32 * NTW / (16 * (4 / WMC)), MTW = (MT + WMC - 1) / WMC;
+    float *part = nullptr;
+    uint32_t *cnt = nullptr, coh = 0, grid = p.tiles;
+    size_t bytes = 0;
+    if (p.splits > 1) {
+        bytes = (size_t)p.tiles * p.splits * 4 * TPW * MTW * 64 * 16;
+        if (bytes > 0xf0000000ull) {
+            set_error("skinny_wide: %zu bytes of split partials exceed the 32-bit offsets", bytes);
+            return RENG_HIP_EINVAL;
+        }
+        int rc = RENG_HIP_OK;
+        part = split_partials(bytes / sizeof(float), st, fixed, &rc);
+        if (rc) return rc;
+        if (fixed && p.tiles > STATIC_TILE_COUNTERS) {
+            set_error("skinny_wide: %u row tiles exceed the %u static tile counters", p.tiles, STATIC_TILE_COUNTERS);
+            return RENG_HIP_EINVAL;
+        }
+        cnt = fixed ? static_tile_counters(&rc) : tile_counters(p.tiles, st, &rc);
+        if (rc) return rc;
+        coh = split_coherence(st, fixed == nullptr);
+        grid = 8 * ((p.tiles + 7) / 8) * p.splits;
+    }
+    hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S>), dim3(grid), dim3(256), 0, st, x, codes, scales, M, N, K, p.tiles,
+                       p.splits, p.cps, y, part, (uint32_t)bytes, cnt, coh);
+    return check_launch("skinny_wide");
 }
 
 template <int F, int MT>
 int launch_wide_mt(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                    uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
-    // 64-row blocks for small matrices (fewer splits: the partials cost more
-    // than the activation re-reads there), else 128 (half the activation
-    // bytes per code) - unless 128-row blocks leave over 30% of the CUs idle
-    // and 96-row ones cover more (Qwen2.5-7B gate/up [18944, 3584]: 148 ->
-    // 198 blocks, M = 64: 26.8 -> 24.1 us). Ring depths from a sweep of 3-6
-    // stages per form on MI355X (Qwen2.5-7B shapes, M = 32 and 64): 4 stages
-    // for the 64- and 96-row forms (M = 64 [3584, 3584] 12.8 -> 11.6 us,
-    // [18944, 3584] 24.2 -> 22.9 us; M = 32 [18944, 3584] 20.7 -> 17.6 us),
-    // 3 for the 128-row one ([3584, 18944] 23.8 -> 22.4 us).
-    if ((uint64_t)N * K <= (16ull << 20)) return launch_wide_cfg<F, MT, 2, 4>(x, codes, scales, M, N, K, y, st, fixed);
-    const uint32_t cus = (uint32_t)device_props().cus, b128 = wide_blocks(N, K, 128);
-    if (10 * b128 < 7 * cus && wide_blocks(N, K, 96) > b128)
-        return launch_wide_cfg<F, MT, 3, 4>(x, codes, scales, M, N, K, y, st, fixed);
-    return launch_wide_cfg<F, MT, 4, 3>(x, codes, scales, M, N, K, y, st, fixed);
+    const WidePlan p = wide_plan(MT, N, K);
+    if constexpr (MT == 1) {
+        if (p.ntw == 4) return launch_wide_cfg<F, 1, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+        return launch_wide_cfg<F, 1, 2, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+    } else {
+        switch (p.ntw) {
+            case 1: return launch_wide_cfg<F, MT, 1, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+            case 3: return launch_wide_cfg<F, MT, 3, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+            case 4: return launch_wide_cfg<F, MT, 4, 3>(x, codes, scales, M, N, K, y, st, fixed, p);
+            default: return launch_wide_cfg<F, MT, 2, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+        }
+    }
 }
 
-// The stage-copy yardstick on the grid skinny_wide would take for this product.
+// The stage-copy yardstick on the blocks skinny_wide would take for this
+// product (its rows per block, ring and splits; a (tiles, splits) grid).
 template <int MT, int NTW, int S>
 int launch_stage_copy_cfg(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K,
-                          uint32_t *sink, hipStream_t st) {
-    const uint32_t tiles = (N + 32 * NTW - 1) / (32 * NTW);
-    const uint32_t chunks = K / CHUNK, cus = (uint32_t)device_props().cus;
-    const uint32_t max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
-    uint32_t splits = cus / tiles;
-    splits = splits < 1 ? 1 : splits > max_splits ? max_splits : splits;
-    const uint32_t cps = (chunks + splits - 1) / splits;
-    splits = (chunks + cps - 1) / cps;
-    hipLaunchKernelGGL((stage_copy_kernel<MT, NTW, S>), dim3(tiles, splits), dim3(256), 0, st, x, codes, M, N, K, cps,
-                       sink);
+                          uint32_t *sink, hipStream_t st, const WidePlan &p) {
+    hipLaunchKernelGGL((stage_copy_kernel<MT, NTW, S>), dim3(p.tiles, p.splits), dim3(256), 0, st, x, codes, M, N, K,
+                       p.cps, sink);
     return check_launch("stage_copy");
 }
 
 template <int MT>
 int launch_stage_copy_mt(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K,
                          uint32_t *sink, hipStream_t st) {
-    if ((uint64_t)N * K <= (16ull << 20)) return launch_stage_copy_cfg<MT, 2, 4>(x, codes, M, N, K, sink, st);
-    const uint32_t cus = (uint32_t)device_props().cus, b128 = wide_blocks(N, K, 128);
-    if (10 * b128 < 7 * cus && wide_blocks(N, K, 96) > b128)
-        return launch_stage_copy_cfg<MT, 3, 4>(x, codes, M, N, K, sink, st);
-    return launch_stage_copy_cfg<MT, 4, 3>(x, codes, M, N, K, sink, st);
+    const WidePlan p = wide_plan(MT, N, K);
+    switch (p.ntw) {
+        case 1: return launch_stage_copy_cfg<MT, 1, 4>(x, codes, M, N, K, sink, st, p);
+        case 3: return launch_stage_copy_cfg<MT, 3, 4>(x, codes, M, N, K, sink, st, p);
+        case 4: return launch_stage_copy_cfg<MT, 4, 3>(x, codes, M, N, K, sink, st, p);
+        default: return launch_stage_copy_cfg<MT, 2, 4>(x, codes, M, N, K, sink, st, p);
+    }
 }
 
 template <int F>
 int launch_wide_f(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                   uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     switch ((M + 15) / 16) {
+        case 1: return launch_wide_mt<F, 1>(x, codes, scales, M, N, K, y, st, fixed);
         case 2: return launch_wide_mt<F, 2>(x, codes, scales, M, N, K, y, st, fixed);
         case 3: return launch_wide_mt<F, 3>(x, codes, scales, M, N, K, y, st, fixed);
         default: return launch_wide_mt<F, 4>(x, codes, scales, M, N, K, y, st, fixed);
@@ -756,9 +875,22 @@ int launch_stage_copy(const uint16_t *x, const uint8_t *codes, uint32_t M, uint3
 }
 
 // 2 <= M <= 16, K % 128 == 0 (rows past M repeat row M - 1 and are not stored).
+// skinny_rows runs a product in one round of whole-K blocks; skinny_wide's
+// one-activation-tile form splits K over blocks and merges the splits in the
+// launch. The split form takes long rows (K >= 8192: Qwen2.5-7B down
+// [3584, 18944] at M = 8 17.9 -> 15.0 us, M = 16 22.3 -> 15.0 us), and for
+// 8 < M <= 16 every product but those whose 16-row tiles fill between half
+// and all of the CUs ([3584, 3584]: 6.5 against 6.9 us; kv [512, 3584]
+// 5.6 -> 5.1 us, gate/up [18944, 3584] 21.5 -> 17.5 us).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
-                       uint32_t K, int format, uint16_t *y, hipStream_t st) {
+                       uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     using namespace skinny;
+    const uint32_t cus = (uint32_t)device_props().cus, t16 = (N + 15) / 16;
+    const bool split = K >= 8192 || (M > 8 && !(t16 <= cus && 2 * t16 > cus));
+    if (split) {
+        if (format == RENG_HIP_E4M3) return launch_wide_mt<RENG_HIP_E4M3, 1>(x, codes, scales, M, N, K, y, st, fixed);
+        return launch_wide_mt<RENG_HIP_E5M2, 1>(x, codes, scales, M, N, K, y, st, fixed);
+    }
     if (M <= 8) {
         if (format == RENG_HIP_E4M3) return launch_ma<RENG_HIP_E4M3, 8>(x, codes, scales, M, N, K, y, st);
         return launch_ma<RENG_HIP_E5M2, 8>(x, codes, scales, M, N, K, y, st);

@@ -217,11 +217,11 @@ def test_skinny_rows_block_shapes(R, M, N, K):
     check_w8a16(R, rng, M, N, K, fmt, sample_cols=None if N * K <= 4096 * 384 else 512)
 
 
-# 16 < M <= 64 (skinny_wide): 64-, 96- and 128-row blocks (96 where 128-row
-# blocks leave CUs idle: N = 18950, K = 1024, with a partial last block), one K
-# split (N past a grid's worth of tiles) and many (the partials and their
-# ordered reduce), the scalar paths for N % 4 != 0, N below one block, 2, 3
-# and 4 activation tiles.
+# 16 < M <= 64 (skinny_wide): 32-, 64-, 96- and 128-row blocks (96 where
+# 128-row blocks leave CUs idle: N = 18950, K = 1024, with a partial last
+# block), one K split (N past a grid's worth of tiles) and many (the partials
+# merged in the launch), the scalar paths for N % 4 != 0, N below one block,
+# 2, 3 and 4 activation tiles.
 @pytest.mark.parametrize("M", [17, 32, 40, 48, 63, 64])
 @pytest.mark.parametrize("N,K", [(48, 4096), (3584, 1152), (4101, 384), (40000, 256), (6000, 2944),
                                  (18950, 1024)])
@@ -229,6 +229,38 @@ def test_skinny_wide_block_shapes(R, M, N, K):
     rng = np.random.default_rng(2000 * M + N + K)
     fmt = E5M2 if (M + N) % 2 else E4M3
     check_w8a16(R, rng, M, N, K, fmt, sample_cols=None if N * K <= 4096 * 384 else 512)
+
+
+# The K splits merged inside the launch: M <= 16 products on the split form
+# (K >= 8192; 8 < M <= 16 outside the band where 16-row tiles fill half to all
+# of the CUs), 16 < M <= 64 with 32-row blocks (few tiles), row tiles not a
+# multiple of the 8 XCDs (padding blocks in the XCD-major grid), a short last
+# split, N % 4 != 0, one row tile in all, and 2 <= M <= 4 on long rows.
+@pytest.mark.parametrize("M", [2, 8, 12, 16, 24, 64])
+@pytest.mark.parametrize("N,K", [(512, 3584), (1000, 8192), (77, 9344), (3000, 2944), (200, 16384)])
+def test_split_merge_shapes(R, M, N, K):
+    rng = np.random.default_rng(3000 * M + N + K)
+    fmt = E4M3 if (M + K // 128) % 2 else E5M2
+    check_w8a16(R, rng, M, N, K, fmt, sample_cols=None if N * K <= 1024 * 8192 else 384)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 512, 3584), (16, 3584, 18944), (8, 1000, 8192), (40, 3584, 3584)])
+def test_split_merge_is_deterministic_and_leaves_its_counters_zeroed(R, M, N, K):
+    """The last block of a row tile adds the splits in split order whichever
+    block it is, and resets the tile's counter: repeated calls, and calls after
+    other split products on the same stream, give the same bits."""
+    rng = np.random.default_rng(M + N + K)
+    q = quantized_weight(rng, N, K, E4M3)
+    x = dev(bf16_bits(rng.standard_normal((M, K)).astype(np.float32)).ravel())
+    c, s = dev(q.codes), dev(q.scales)
+    first = R.gemm_w8a16(x, c, s, M, N, K, E4M3).clone()
+    for _ in range(3):
+        assert torch.equal(R.gemm_w8a16(x, c, s, M, N, K, E4M3), first)
+    q2 = quantized_weight(rng, 700, 4096, E5M2)
+    x2 = dev(bf16_bits(rng.standard_normal((24, 4096)).astype(np.float32)).ravel())
+    R.gemm_w8a16(x2, dev(q2.codes), dev(q2.scales), 24, 700, 4096, E5M2)
+    assert torch.equal(R.gemm_w8a16(x, c, s, M, N, K, E4M3), first)
+    torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("M", [8, 64])
