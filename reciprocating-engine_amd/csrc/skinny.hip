@@ -392,28 +392,23 @@ int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint
 __device__ __forceinline__ uint32_t swz8(uint32_t r) { return (r ^ ((r >> 3) & 1)) & 7; }
 
 // The tile's last block learns it here; its frag then hold the sums over the
-// splits. Slot (tile, split) holds waves x NF x 64 f32x4, fragment f of lane l
-// of wave w at (w NF + f) 64 + l. Every block of the tile calls this (it has
-// barriers). part is addressed through a buffer resource of part_bytes, so
-// the loads of a group past the last split fetch nothing.
-template <int NF>
+// splits. Slot (tile, split) holds 4 waves x NF x 64 f32x4, fragment f of
+// lane l of wave w at (w NF + f) 64 + l. Every block of the tile calls this
+// (it has barriers). part is addressed through a buffer resource of
+// part_bytes, so the loads of a group past the last split fetch nothing.
+template <int NF, int COH>
 __device__ __forceinline__ bool merge_splits(f32x4 (&frag)[NF], float *part, uint32_t part_bytes, uint32_t *cnt,
-                                             uint32_t tile, uint32_t split, uint32_t splits, uint32_t coh,
-                                             uint32_t *flag) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+                                             uint32_t tile, uint32_t split, uint32_t splits, uint32_t *flag) {
+    constexpr uint32_t WAVES = 4;   // skinny_wide's block
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, 0, part_bytes, 0x00020000);
-    const uint32_t slot = (uint32_t)waves * NF * 64 * 16;   // bytes per (tile, split)
+    constexpr uint32_t slot = WAVES * NF * 64 * 16;   // bytes per (tile, split)
     const uint32_t lo = (uint32_t)(wave * NF * 64 + lane) * 16;
     const uint32_t mine = (tile * splits + split) * slot + lo;
-    if (coh) {
+    constexpr int ST = COH ? 16 : 0, LD = COH ? 16 : 1;   // sc1 both ways, or plain stores and sc0 loads
 #pragma unroll
-        for (int f = 0; f < NF; ++f)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, frag[f]), rs, mine + f * 1024, 0, 16);
-    } else {
-#pragma unroll
-        for (int f = 0; f < NF; ++f)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, frag[f]), rs, mine + f * 1024, 0, 0);
-    }
+    for (int f = 0; f < NF; ++f)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, frag[f]), rs, mine + f * 1024, 0, ST);
     asm volatile("" ::: "memory");
     wait_vmcnt<0>();   // this wave's fragments are in the cache the last block reads
     __syncthreads();
@@ -424,29 +419,22 @@ __device__ __forceinline__ bool merge_splits(f32x4 (&frag)[NF], float *part, uin
     __syncthreads();
     if (!*flag) return false;
     asm volatile("" ::: "memory");
-    // Eight splits' fragments requested together, then added in order.
+    // GS splits' fragments (32 loads per lane at most) requested together,
+    // then added in order.
+    constexpr int GS = NF >= 16 ? 2 : NF >= 8 ? 4 : 8;
     const uint32_t base = tile * splits * slot + lo;
     constexpr uint32_t PAST = 0xf8000000u;   // past any part_bytes (<= 0xf0000000): loads nothing
-    for (uint32_t s0 = 0; s0 < splits; s0 += 8) {
-        u32x4 v[8][NF];
-        if (coh) {
+    for (uint32_t s0 = 0; s0 < splits; s0 += GS) {
+        u32x4 v[GS][NF];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t off = s0 + i < splits ? base + (s0 + i) * slot : PAST;
+        for (int i = 0; i < GS; ++i) {
+            const uint32_t off = s0 + i < splits ? base + (s0 + i) * slot : PAST;
 #pragma unroll
-                for (int f = 0; f < NF; ++f) v[i][f] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + f * 1024, 0, 16);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t off = s0 + i < splits ? base + (s0 + i) * slot : PAST;
-#pragma unroll
-                for (int f = 0; f < NF; ++f) v[i][f] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + f * 1024, 0, 1);
-            }
+            for (int f = 0; f < NF; ++f) v[i][f] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + f * 1024, 0, LD);
         }
         asm volatile("" ::: "memory");   // all of the group's loads before the first add
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < GS; ++i) {
             const bool ok = s0 + i < splits, first = s0 + i == 0;
 #pragma unroll
             for (int f = 0; f < NF; ++f) {
@@ -460,12 +448,12 @@ __device__ __forceinline__ bool merge_splits(f32x4 (&frag)[NF], float *part, uin
     return true;
 }
 
-template <int F, int MT, int NTW, int S>
+template <int F, int MT, int NTW, int S, int COH>
 __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes,
                                                    const float *__restrict__ scales, uint32_t M, uint32_t N,
                                                    uint32_t K, uint32_t tiles, uint32_t splits, uint32_t cps,
                                                    uint16_t *__restrict__ y, float *part, uint32_t part_bytes,
-                                                   uint32_t *cnt, uint32_t coh) {
+                                                   uint32_t *cnt) {
     constexpr int BK = CHUNK, R = 32 * NTW, AR = 16 * MT;
     constexpr int WB = R * BK, AB = AR * BK * 2, SLOT = WB + AB;
     constexpr int WC = R / 8, AC = AR / 4;          // copies per stage (block)
@@ -592,7 +580,7 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
         compute(st);
     }
 
-    if (splits > 1 && !merge_splits<TPW * MTW>(acc, part, part_bytes, cnt, tile, split, splits, coh, &last_flag))
+    if (splits > 1 && !merge_splits<TPW * MTW, COH>(acc, part, part_bytes, cnt, tile, split, splits, &last_flag))
         return;
 
     // Lane holds column m = 16 mt + l % 16 and rows n = 4 (l / 16) + e.
@@ -806,8 +794,12 @@ int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales
         coh = split_coherence(st, fixed == nullptr);
         grid = 8 * ((p.tiles + 7) / 8) * p.splits;
     }
-    hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S>), dim3(grid), dim3(256), 0, st, x, codes, scales, M, N, K, p.tiles,
-                       p.splits, p.cps, y, part, (uint32_t)bytes, cnt, coh);
+    if (coh)
+        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 1>), dim3(grid), dim3(256), 0, st, x, codes, scales, M, N, K,
+                           p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
+    else
+        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 0>), dim3(grid), dim3(256), 0, st, x, codes, scales, M, N, K,
+                           p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
     return check_launch("skinny_wide");
 }
 
