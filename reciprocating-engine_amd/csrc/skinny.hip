@@ -392,14 +392,14 @@ int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint
 __device__ __forceinline__ uint32_t swz8(uint32_t r) { return (r ^ ((r >> 3) & 1)) & 7; }
 
 // The tile's last block learns it here; its frag then hold the sums over the
-// splits. Slot (tile, split) holds 4 waves x NF x 64 f32x4, fragment f of
+// splits. Slot (tile, split) holds NWV waves x NF x 64 f32x4, fragment f of
 // lane l of wave w at (w NF + f) 64 + l. Every block of the tile calls this
 // (it has barriers). part is addressed through a buffer resource of
 // part_bytes, so the loads of a group past the last split fetch nothing.
-template <int NF, int COH>
+template <int NF, int COH, int NWV>
 __device__ __forceinline__ bool merge_splits(f32x4 (&frag)[NF], float *part, uint32_t part_bytes, uint32_t *cnt,
                                              uint32_t tile, uint32_t split, uint32_t splits, uint32_t *flag) {
-    constexpr uint32_t WAVES = 4;   // skinny_wide's block
+    constexpr uint32_t WAVES = NWV;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, 0, part_bytes, 0x00020000);
     constexpr uint32_t slot = WAVES * NF * 64 * 16;   // bytes per (tile, split)
@@ -448,8 +448,8 @@ __device__ __forceinline__ bool merge_splits(f32x4 (&frag)[NF], float *part, uin
     return true;
 }
 
-template <int F, int MT, int NTW, int S, int COH>
-__global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes,
+template <int F, int MT, int NTW, int S, int COH, int NWV>
+__global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes,
                                                    const float *__restrict__ scales, uint32_t M, uint32_t N,
                                                    uint32_t K, uint32_t tiles, uint32_t splits, uint32_t cps,
                                                    uint16_t *__restrict__ y, float *part, uint32_t part_bytes,
@@ -457,10 +457,10 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
     constexpr int BK = CHUNK, R = 32 * NTW, AR = 16 * MT;
     constexpr int WB = R * BK, AB = AR * BK * 2, SLOT = WB + AB;
     constexpr int WC = R / 8, AC = AR / 4;          // copies per stage (block)
-    static_assert(WC % 4 == 0 && AC % 4 == 0, "copies split evenly over 4 waves");
-    constexpr int C = (WC + AC) / 4;                // copies per stage per wave
+    static_assert(WC % NWV == 0 && AC % NWV == 0, "copies split evenly over the waves");
+    constexpr int C = (WC + AC) / NWV;              // copies per stage per wave
     static_assert(S >= 2 && (S - 2) * C < 64, "vmcnt");
-    constexpr int WMC = MT >= 2 ? 2 : 1, WNC = 4 / WMC;
+    constexpr int WMC = MT >= 2 ? 2 : 1, WNC = NWV / WMC;
     constexpr int TPW = R / (16 * WNC);             // 16-row tiles per wave
     static_assert(TPW >= 1 && TPW * 16 * WNC == R, "rows split evenly over the wave rows");
     constexpr int MTW = (MT + WMC - 1) / WMC;       // activation tiles per wave
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
     uint32_t dst[C], unit[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        const int q = wave + 4 * c;
+        const int q = wave + NWV * c;
         if (q < WC) {
             const uint32_t rr = q * 8 + lane / 8, p = (lane % 8) ^ swz8(rr);
             uint32_t n = n0 + rr;
@@ -580,7 +580,7 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
         compute(st);
     }
 
-    if (splits > 1 && !merge_splits<TPW * MTW, COH>(acc, part, part_bytes, cnt, tile, split, splits, &last_flag))
+    if (splits > 1 && !merge_splits<TPW * MTW, COH, NWV>(acc, part, part_bytes, cnt, tile, split, splits, &last_flag))
         return;
 
     // Lane holds column m = 16 mt + l % 16 and rows n = 4 (l / 16) + e.
@@ -617,15 +617,15 @@ __global__ __launch_bounds__(256) void skinny_wide(const uint16_t *__restrict__ 
 // with no fragment reads, decodes, MFMAs or output. Its time is the floor that
 // the kernel's data movement alone sets. sink gets one word if a (never
 // matching) value turns up, which keeps the copies live.
-template <int MT, int NTW, int S>
-__global__ __launch_bounds__(256) void stage_copy_kernel(const uint16_t *__restrict__ x,
-                                                         const uint8_t *__restrict__ codes, uint32_t M, uint32_t N,
-                                                         uint32_t K, uint32_t cps, uint32_t *sink) {
+template <int MT, int NTW, int S, int NWV>
+__global__ __launch_bounds__(64 * NWV) void stage_copy_kernel(const uint16_t *__restrict__ x,
+                                                              const uint8_t *__restrict__ codes, uint32_t M,
+                                                              uint32_t N, uint32_t K, uint32_t cps, uint32_t *sink) {
     constexpr int BK = CHUNK, R = 32 * NTW, AR = 16 * MT;
     constexpr int WB = R * BK, AB = AR * BK * 2, SLOT = WB + AB;
     constexpr int WC = R / 8, AC = AR / 4;
-    constexpr int C = (WC + AC) / 4;
-    static_assert(WC % 4 == 0 && AC % 4 == 0 && S >= 2 && (S - 2) * C < 64, "as skinny_wide");
+    constexpr int C = (WC + AC) / NWV;
+    static_assert(WC % NWV == 0 && AC % NWV == 0 && S >= 2 && (S - 2) * C < 64, "as skinny_wide");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * SLOT];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -637,7 +637,7 @@ __global__ __launch_bounds__(256) void stage_copy_kernel(const uint16_t *__restr
     uint32_t dst[C], unit[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        const int q = wave + 4 * c;
+        const int q = wave + NWV * c;
         if (q < WC) {
             const uint32_t rr = q * 8 + lane / 8, p = (lane % 8) ^ swz8(rr);
             uint32_t n = n0 + rr;
@@ -720,17 +720,22 @@ uint32_t split_coherence(hipStream_t st, bool may_check) {
 // A launch of skinny_wide: R = 32 ntw rows per block, an s-slot ring, the
 // product's row tiles and K splits (cps chunks each).
 struct WidePlan {
-    uint32_t ntw, s, tiles, splits, cps;
+    uint32_t ntw, s, nwv, tiles, splits, cps;
 };
 
 // Rows per block first: for 16 < M <= 64 (mt >= 2), 64 on small matrices (the
 // partials of more splits cost more than the activation re-reads) or 32 where
 // 64-row blocks split as far as they go would keep under half the CUs busy
 // (Qwen2.5-7B kv [512, 3584] at M = 64: 8.84 -> 6.94 us); on large ones 128
-// (half the activation bytes per code) unless 128-row blocks leave over 30%
-// of the CUs idle and 96-row ones cover more (Qwen2.5-7B gate/up [18944, 3584]:
-// 148 -> 198 blocks). For M <= 16 (mt = 1, one 16-row activation tile) 64,
-// or 128 on large matrices. Ring depths from sweeps of 3-6 stages on MI355X.
+// (half the activation bytes per code). With an even number of activation
+// tiles the 64- and 128-row blocks run 8 waves (two per SIMD, each issuing
+// half the copies and computing half the tiles): the copy stream is what
+// bounds these products, and 8 waves move it 5-10% faster than 4 (M = 64
+// Qwen2.5-7B q/o 10.8 -> 10.0 us, down 25.3 -> 23.4 us, gate/up 25.3 -> 23.2 us
+// against 96-row 4-wave blocks). With 4 waves (mt = 3) 128-row blocks give way
+// to 96-row ones where they leave over 30% of the CUs idle and 96-row ones
+// cover more. For M <= 16 (mt = 1, one 16-row activation tile) 64, or 128 on
+// large matrices, 4 waves. Ring depths from sweeps of 3-6 stages on MI355X.
 // Then the splits: as many as keep each XCD's share of the grid (ceil(tiles /
 // 8) row tiles times the splits) within its CUs, so the grid runs in one
 // round, with at least 4 chunks (512 codes) per split.
@@ -745,10 +750,12 @@ WidePlan wide_plan(uint32_t mt, uint32_t N, uint32_t K) {
         return sp < 1 ? 1u : sp > max_splits ? max_splits : sp;
     };
     const bool small = (uint64_t)N * K <= (16ull << 20);
-    WidePlan p{2, 4, 0, 1, chunks};
+    WidePlan p{2, 4, 4, 0, 1, chunks};
     if (mt >= 2) {
         if (small) {
             if (2 * tiles_of(64) * max_splits < cus) p.ntw = 1;
+        } else if (mt % 2 == 0) {
+            p.ntw = 4;
         } else {
             const uint32_t b128 = tiles_of(128) * splits_of(128), b96 = tiles_of(96) * splits_of(96);
             if (10 * b128 < 7 * cus && b96 > b128) {
@@ -758,6 +765,7 @@ WidePlan wide_plan(uint32_t mt, uint32_t N, uint32_t K) {
                 p.s = 3;
             }
         }
+        if (mt % 2 == 0 && p.ntw % 2 == 0) p.nwv = 8;
     } else if (!small) {
         p.ntw = 4;
     }
@@ -769,15 +777,15 @@ WidePlan wide_plan(uint32_t mt, uint32_t N, uint32_t K) {
     return p;
 }
 
-template <int F, int MT, int NTW, int S>
+template <int F, int MT, int NTW, int S, int NWV>
 int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                     uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed, const WidePlan &p) {
-    constexpr uint32_t WMC = MT >= 2 ? 2 : 1, TPW = 32 * NTW / (16 * (4 / WMC)), MTW = (MT + WMC - 1) / WMC;
+    constexpr uint32_t WMC = MT >= 2 ? 2 : 1, TPW = 32 * NTW / (16 * (NWV / WMC)), MTW = (MT + WMC - 1) / WMC;
     float *part = nullptr;
     uint32_t *cnt = nullptr, coh = 0, grid = p.tiles;
     size_t bytes = 0;
     if (p.splits > 1) {
-        bytes = (size_t)p.tiles * p.splits * 4 * TPW * MTW * 64 * 16;
+        bytes = (size_t)p.tiles * p.splits * NWV * TPW * MTW * 64 * 16;
         if (bytes > 0xf0000000ull) {
             set_error("skinny_wide: %zu bytes of split partials exceed the 32-bit offsets", bytes);
             return RENG_HIP_EINVAL;
@@ -795,11 +803,11 @@ int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales
         grid = 8 * ((p.tiles + 7) / 8) * p.splits;
     }
     if (coh)
-        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 1>), dim3(grid), dim3(256), 0, st, x, codes, scales, M, N, K,
-                           p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
+        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 1, NWV>), dim3(grid), dim3(64 * NWV), 0, st, x, codes, scales,
+                           M, N, K, p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
     else
-        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 0>), dim3(grid), dim3(256), 0, st, x, codes, scales, M, N, K,
-                           p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
+        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 0, NWV>), dim3(grid), dim3(64 * NWV), 0, st, x, codes, scales,
+                           M, N, K, p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
     return check_launch("skinny_wide");
 }
 
@@ -808,25 +816,31 @@ int launch_wide_mt(const uint16_t *x, const uint8_t *codes, const float *scales,
                    uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     const WidePlan p = wide_plan(MT, N, K);
     if constexpr (MT == 1) {
-        if (p.ntw == 4) return launch_wide_cfg<F, 1, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
-        return launch_wide_cfg<F, 1, 2, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+        if (p.ntw == 4) return launch_wide_cfg<F, 1, 4, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+        return launch_wide_cfg<F, 1, 2, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+    } else if constexpr (MT % 2 == 0) {
+        switch (p.ntw) {
+            case 1: return launch_wide_cfg<F, MT, 1, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+            case 4: return launch_wide_cfg<F, MT, 4, 4, 8>(x, codes, scales, M, N, K, y, st, fixed, p);
+            default: return launch_wide_cfg<F, MT, 2, 4, 8>(x, codes, scales, M, N, K, y, st, fixed, p);
+        }
     } else {
         switch (p.ntw) {
-            case 1: return launch_wide_cfg<F, MT, 1, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
-            case 3: return launch_wide_cfg<F, MT, 3, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
-            case 4: return launch_wide_cfg<F, MT, 4, 3>(x, codes, scales, M, N, K, y, st, fixed, p);
-            default: return launch_wide_cfg<F, MT, 2, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+            case 1: return launch_wide_cfg<F, MT, 1, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+            case 3: return launch_wide_cfg<F, MT, 3, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+            case 4: return launch_wide_cfg<F, MT, 4, 3, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
+            default: return launch_wide_cfg<F, MT, 2, 4, 4>(x, codes, scales, M, N, K, y, st, fixed, p);
         }
     }
 }
 
 // The stage-copy yardstick on the blocks skinny_wide would take for this
 // product (its rows per block, ring and splits; a (tiles, splits) grid).
-template <int MT, int NTW, int S>
+template <int MT, int NTW, int S, int NWV>
 int launch_stage_copy_cfg(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K,
                           uint32_t *sink, hipStream_t st, const WidePlan &p) {
-    hipLaunchKernelGGL((stage_copy_kernel<MT, NTW, S>), dim3(p.tiles, p.splits), dim3(256), 0, st, x, codes, M, N, K,
-                       p.cps, sink);
+    hipLaunchKernelGGL((stage_copy_kernel<MT, NTW, S, NWV>), dim3(p.tiles, p.splits), dim3(64 * NWV), 0, st, x, codes,
+                       M, N, K, p.cps, sink);
     return check_launch("stage_copy");
 }
 
@@ -834,11 +848,19 @@ template <int MT>
 int launch_stage_copy_mt(const uint16_t *x, const uint8_t *codes, uint32_t M, uint32_t N, uint32_t K,
                          uint32_t *sink, hipStream_t st) {
     const WidePlan p = wide_plan(MT, N, K);
-    switch (p.ntw) {
-        case 1: return launch_stage_copy_cfg<MT, 1, 4>(x, codes, M, N, K, sink, st, p);
-        case 3: return launch_stage_copy_cfg<MT, 3, 4>(x, codes, M, N, K, sink, st, p);
-        case 4: return launch_stage_copy_cfg<MT, 4, 3>(x, codes, M, N, K, sink, st, p);
-        default: return launch_stage_copy_cfg<MT, 2, 4>(x, codes, M, N, K, sink, st, p);
+    if constexpr (MT % 2 == 0) {
+        switch (p.ntw) {
+            case 1: return launch_stage_copy_cfg<MT, 1, 4, 4>(x, codes, M, N, K, sink, st, p);
+            case 4: return launch_stage_copy_cfg<MT, 4, 4, 8>(x, codes, M, N, K, sink, st, p);
+            default: return launch_stage_copy_cfg<MT, 2, 4, 8>(x, codes, M, N, K, sink, st, p);
+        }
+    } else {
+        switch (p.ntw) {
+            case 1: return launch_stage_copy_cfg<MT, 1, 4, 4>(x, codes, M, N, K, sink, st, p);
+            case 3: return launch_stage_copy_cfg<MT, 3, 4, 4>(x, codes, M, N, K, sink, st, p);
+            case 4: return launch_stage_copy_cfg<MT, 4, 3, 4>(x, codes, M, N, K, sink, st, p);
+            default: return launch_stage_copy_cfg<MT, 2, 4, 4>(x, codes, M, N, K, sink, st, p);
+        }
     }
 }
 
