@@ -372,8 +372,8 @@ int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint
 //   codes: R / 8 copies of 8 rows x 128 bytes, piece p of row r in slot p ^ swz8(r);
 //   activation: 16 MT rows (>= M repeat row M - 1), 4 rows x 256 bytes per copy,
 //     8-element piece p of row r in slot p ^ (r % 16);
-// spread over the waves. The waves form a WNC x WMC grid (2 x 2 for MT >= 2,
-// 4 x 1 for MT = 1): wave (wn, wm) computes rows [wn R / WNC, +R / WNC)
+// spread over the NWV waves. The waves form a WNC x WMC grid (WMC = 2 for
+// MT >= 2, 1 for MT = 1): wave (wn, wm) computes rows [wn R / WNC, +R / WNC)
 // against activation tiles wm, wm + WMC, ... (< MT).
 //
 // Blocks split K until the grid fills the CUs (split s takes chunks
@@ -387,8 +387,21 @@ int launch_ma(const uint16_t *x, const uint8_t *codes, const float *scales, uint
 // are dealt to the 8 XCDs round-robin) and takes tile (b / 8 / splits) * 8 +
 // b % 8, so a tile's splits share one XCD's L2, where the partials go with
 // plain stores and come back with L1-bypassing (sc0) loads. If the device was
-// not seen to place workgroups that way (xcd_placement), the partials go
+// not seen to place workgroups that way (split_coherence), the partials go
 // through agent-coherent (sc1) stores and loads instead.
+//
+// Why the last block sees every partial: each block's partial stores have
+// completed (vmcnt 0: acknowledged by the L2, or with sc1 by memory) before
+// its count is issued; the count is one atomic read-modify-write per tile, so
+// the block that sees splits - 1 counts before its own comes after every
+// other block's count; and it issues its loads only once its own count has
+// returned. With COH 0 every block of the tile runs on one XCD and so writes
+// and reads the same L2 (the loads skip the L1); with COH 1 the sc1 stores
+// and loads are coherent across XCDs. This is gfx950's ordering of these
+// accesses, not a release / acquire pair of the HIP memory model: at agent
+// scope that pair would write back and invalidate the XCD's whole L2
+// (buffer_wbl2 / buffer_inv) in every block. The split tests call each
+// product repeatedly and check every output and bit-identical repeats.
 __device__ __forceinline__ uint32_t swz8(uint32_t r) { return (r ^ ((r >> 3) & 1)) & 7; }
 
 // The tile's last block learns it here; its frag then hold the sums over the
