@@ -8,6 +8,8 @@ the reference probe does (fp8_probe.rs:242-248, 295-298). Exactness of the
 in-register decode is checked on its own: a one-hot activation reads every
 finite code back bit for bit.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -261,6 +263,57 @@ def test_split_merge_is_deterministic_and_leaves_its_counters_zeroed(R, M, N, K)
     R.gemm_w8a16(x2, dev(q2.codes), dev(q2.scales), 24, 700, 4096, E5M2)
     assert torch.equal(R.gemm_w8a16(x, c, s, M, N, K, E4M3), first)
     torch.cuda.synchronize()
+
+
+_FIRST_CALL_CHILD = r"""
+import ctypes, os, sys
+root = sys.argv[1]
+for p in (os.path.join(root, "reciprocating-engine_amd"), os.path.join(root, "oracle"), os.path.join(root, "tests")):
+    sys.path.insert(0, p)
+import os
+
+import numpy as np
+import torch
+import oracle as O
+import reng_hip as R
+from helpers import bf16_bits
+torch.cuda.set_device(0)
+L = R.lib()
+rng = np.random.default_rng(7)
+st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+outs = []
+for (M, N, K) in ((64, 3584, 3584), (8, 1000, 8192), (24, 512, 3584)):
+    w = bf16_bits((rng.standard_normal((N, K)) * 0.02).astype(np.float32)).ravel()
+    q = O.quantize(w, N, K, 0, "pcs")
+    x = torch.from_numpy(bf16_bits(rng.standard_normal((M, K)).astype(np.float32)).ravel().view(np.int16)).cuda()
+    c, s = torch.from_numpy(q.codes).cuda(), torch.from_numpy(q.scales).cuda()
+    y = torch.empty(M * N, dtype=torch.int16, device="cuda")
+    rc = L.reng_hip_gemm_w8a16_noalloc(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(c.data_ptr()),
+                                       ctypes.c_void_p(s.data_ptr()), M, N, K, 0, ctypes.c_void_p(y.data_ptr()), st)
+    assert rc == 0, L.reng_hip_last_error()
+    outs.append((x, c, s, M, N, K, y))
+torch.cuda.synchronize()
+for x, c, s, M, N, K, y in outs:
+    want = R.gemm_w8a16(x, c, s, M, N, K, "e4m3")
+    torch.cuda.synchronize()
+    assert torch.equal(y, want.view(torch.int16)), (M, N, K)
+print("first-call products equal", flush=True)
+"""
+
+
+def test_split_merge_before_the_placement_check_matches_after_it():
+    """The first split products of a process, through the allocation-free entry
+    (which never runs the XCD placement check), merge their partials with
+    agent-coherent accesses; the allocating entry then checks the placement
+    and merges through the XCD's L2. Run in a fresh process so that nothing
+    has checked the placement yet: both give the same bits."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CHILD, root], capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "first-call products equal" in r.stdout
 
 
 @pytest.mark.parametrize("M", [8, 64])
