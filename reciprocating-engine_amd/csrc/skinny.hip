@@ -718,6 +718,7 @@ uint32_t split_coherence(hipStream_t st, bool may_check) {
     uint32_t *d = nullptr;
     if (hipMalloc(&d, G * sizeof(uint32_t)) != hipSuccess) return 1u;
     std::vector<uint32_t> h(G, 0xffffffffu);
+    (void)hipGetLastError();   // the launch check below sees this launch's error only
     hipLaunchKernelGGL(xcc_probe, dim3(G), dim3(64), 0, st, d);
     const bool ran = hipGetLastError() == hipSuccess &&
                      hipMemcpyAsync(h.data(), d, G * sizeof(uint32_t), hipMemcpyDeviceToHost, st) == hipSuccess &&
@@ -744,8 +745,8 @@ struct WidePlan {
 // tiles the 64- and 128-row blocks run 8 waves (two per SIMD, each issuing
 // half the copies and computing half the tiles): the copy stream is what
 // bounds these products, and 8 waves move it 5-10% faster than 4 (M = 64
-// Qwen2.5-7B q/o 10.8 -> 10.0 us, down 25.3 -> 23.4 us, gate/up 25.3 -> 23.2 us
-// against 96-row 4-wave blocks). With 4 waves (mt = 3) 128-row blocks give way
+// Qwen2.5-7B q/o 10.8 -> 10.0 us, down 25.3 -> 23.4 us; gate/up 23.3 us in
+// 96-row 4-wave blocks -> 22.2 us in 128-row 8-wave ones, same-box replays). With 4 waves (mt = 3) 128-row blocks give way
 // to 96-row ones where they leave over 30% of the CUs idle and 96-row ones
 // cover more. For M <= 16 (mt = 1, one 16-row activation tile) 64, or 128 on
 // large matrices, 4 waves. Ring depths from sweeps of 3-6 stages on MI355X.
