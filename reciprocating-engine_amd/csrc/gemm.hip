@@ -380,23 +380,32 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 
 // ------------------------------------------------------------------ GEMV, M = 1
 
-// One wave per output row, every 1 KB chunk of the row (CPR of them, K <=
-// 16384) requested at the start. In issue order: the row's scale, this
-// thread's share of the activation (into registers, then LDS), the row's
-// codes; the activation is written to LDS and the block barrier waits on LDS
-// only, so the codes stay in flight through it. Every load is an ordinary
-// (compiler-tracked) load, issued unconditionally (indices clamped), so the
-// compiler waits for chunk c alone before consuming it while the later chunks
-// are still in flight. Measured on MI355X against the former walk (R rows per
-// wave in U-chunk steps, untracked loads): [14336, 4096] 10.64 -> 10.12 us,
-// [4096, 4096] 4.92 -> 4.46 us, [4096, 14336] 10.9 us both, with a plain
-// one-launch read of the same codes at 9.5-9.6 us.
+// One wave per output row; the row's CPR 1 KB chunks (K <= 16384) stream
+// through a window of GEMV_WINDOW chunks: the first min(CPR, GEMV_WINDOW) are
+// requested at the start, and chunk c + GEMV_WINDOW is requested just before
+// chunk c is consumed. In issue order: the row's scale, this thread's share of
+// the activation (into registers, then LDS), the row's first chunks; the
+// activation is written to LDS and the block barrier waits on LDS only, so the
+// codes stay in flight through it. Every load is an ordinary (compiler-tracked)
+// load, issued unconditionally (indices clamped), so the compiler waits for
+// chunk c alone before consuming it while the later chunks are still in
+// flight. Measured on MI355X against the former walk (R rows per wave in
+// U-chunk steps, untracked loads): [14336, 4096] 10.64 -> 10.12 us, [4096,
+// 4096] 4.92 -> 4.46 us, with a plain one-launch read of the same codes at
+// 9.5-9.6 us. On 14 KB rows ([4096, 14336]) the whole row in flight served the
+// rows in no useful order (block end times spread over 4 us) and took 10.6-11.3
+// us; a window of 10 chunks takes 10.3 (7: 10.45, 12: 10.33, 14: 10.65).
+// What is left over the plain read on both shapes is the stores of y: the
+// same kernel with them taken out takes 9.87 / 10.04 us, as does a load-only
+// variant that stores y (9.94 / 10.18), against 9.65 / 9.95 without them.
 //
 // A lane takes the same 16 codes of every 1 KB chunk (k = 1024 c + 16 lane ..
 // + 16) and adds the products in gemv_w8a16's order (chunks in order, even and
 // odd words into two accumulators, then wave_sum_dpp), so the two kernels give
 // the same bits and the fused forms of gemv_w8a16 equal this GEMV followed by
 // their epilogue. A ragged last chunk (K % 1024 != 0) masks the lanes past K.
+constexpr int GEMV_WINDOW = 10;
+
 template <int F, int CPR, int WPB>
 // (No __restrict__ on the inputs: loads through a restrict pointer to const may
 // be treated as invariant and moved across the compiler barriers that fix the
@@ -424,12 +433,13 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *x, const u
     asm volatile("" ::: "memory");
     const u32x4 *wr = reinterpret_cast<const u32x4 *>(codes + (size_t)nr * K);
     u32x4 q[CPR];
-#pragma unroll
-    for (int c = 0; c < CPR; ++c) {
+    auto request = [&](int c) {
         const uint32_t lc = c == CPR - 1 && lane >= live ? live - 1 : lane;
         q[c] = __builtin_nontemporal_load(wr + 64 * c + lc);
         asm volatile("" ::: "memory");   // issued in chunk order, the order they are consumed in
-    }
+    };
+#pragma unroll
+    for (int c = 0; c < CPR && c < GEMV_WINDOW; ++c) request(c);
 #pragma unroll
     for (uint32_t j = 0; j < XPT; ++j) {
         const uint32_t i = tid + j * 64 * WPB;
@@ -442,6 +452,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *x, const u
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
+        if (c + GEMV_WINDOW < CPR) request(c + GEMV_WINDOW);
         uint32_t wv[8];
         decode16<F>(q[c], wv);
         u32x4 xa = xs[128 * c + 2 * lane], xb = xs[128 * c + 2 * lane + 1];
