@@ -30,6 +30,7 @@
 #include "common.h"
 #include "gemm.h"
 #include "mfma_pipe.h"
+#include "tile_order.h"
 
 namespace reng {
 
@@ -325,19 +326,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_fp8_wide(const uint8_t *_
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / T::WGN, wn = wave % T::WGN;
 
-    // XCD-major tile order: XCD x takes a contiguous run of tiles, m fastest
-    // (as gemm_fp8_mfma); or, with mapm > 0, a block of mapm m-tiles by
-    // per / mapm n-tiles (the launcher passes mapm only where those blocks
-    // tile the grid exactly), when that reads fewer operand rows per XCD.
-    const uint32_t x = blockIdx.x % XCDS, l = blockIdx.x / XCDS;
-    const uint32_t per = tiles / XCDS, rem = tiles % XCDS;
-    const uint32_t tile = x * per + (x < rem ? x : rem) + l;
-    uint32_t mt = tile % tiles_m, nt = tile / tiles_m;
-    if (mapm) {
-        const uint32_t rgm = tiles_m / mapm, gn = per / mapm;
-        mt = (x % rgm) * mapm + l % mapm;
-        nt = (x / rgm) * gn + l / mapm;
-    }
+    // XCD-major tile order (wide_tile_of, tile_order.h): XCD x takes a
+    // contiguous run of tiles, m fastest (as gemm_fp8_mfma), or a block of mapm
+    // m-tiles by per / mapm n-tiles where the launcher found that to read fewer
+    // operand rows per XCD.
+    uint32_t mt, nt;
+    wide_tile_of(blockIdx.x, tiles_m, tiles, mapm, mt, nt);
     const uint32_t m0 = mt * BM, n0 = nt * BN;
     const uint32_t n = K / BK;
 
@@ -543,34 +537,11 @@ WideCand wide_cand(const Fp8Args &g, float c0, float c1) {
     return WideCand{wide_fits<WM, WN, 128, WGM, WGN>(g), (uint32_t)T::BM, (uint32_t)T::BN, c0, c1};
 }
 
-// The 2-D XCD blocks for gemm_fp8_wide's tile order: the number of m-tiles
-// per XCD block (0 keeps the m-fastest runs), chosen to minimize the operand
-// rows an XCD reads (mapm BM rows of a plus per / mapm BN rows of b), among
-// blocks that tile the grid exactly (8 equal runs, mapm dividing the run and
-// tiles_m, the XCD blocks 8 / (tiles_m / mapm) wide in n). On the kv
-// projection [1024, 1024, 5120] (64 x 64 tiles: 16 m-tiles of which an XCD's
-// run of 32 covers all, plus 2 n-tiles) blocks of 4 x 8 read 768 rows per XCD
-// instead of 1152: 15.0 -> 14.4-14.5 us. On the larger shapes the m-fastest
-// runs already read the fewest rows.
-inline uint32_t wide_mapm(uint32_t tiles_m, uint32_t tiles_n, uint32_t bm, uint32_t bn) {
-    const uint32_t tiles = tiles_m * tiles_n;
-    if (tiles % XCDS) return 0;
-    const uint32_t per = tiles / XCDS;
-    // The m-fastest run: all m-tiles it touches (at most tiles_m) and its n-columns.
-    const uint32_t cm = per < tiles_m ? per : tiles_m;
-    const uint32_t cn = (per + tiles_m - 1) / tiles_m + (per % tiles_m ? 1 : 0);
-    uint64_t best = (uint64_t)cm * bm + (uint64_t)cn * bn;
-    uint32_t pick = 0;
-    for (uint32_t m = 1; m <= tiles_m && m <= per; ++m) {
-        if (tiles_m % m || per % m) continue;
-        const uint32_t rgm = tiles_m / m;
-        if (XCDS % rgm || (XCDS / rgm) * (per / m) != tiles_n) continue;
-        const uint64_t c = (uint64_t)m * bm + (uint64_t)(per / m) * bn;
-        if (c < best) best = c, pick = m;
-    }
-    return pick;
-}
-
+// 2-D XCD blocks of tiles (wide_mapm, tile_order.h): on the kv projection
+// [1024, 1024, 5120] (64 x 64 tiles: 16 m-tiles of which an XCD's run of 32
+// covers all, plus 2 n-tiles) blocks of 4 x 8 read 768 operand rows per XCD
+// instead of 1152: 15.0 -> 14.3-14.5 us. On the larger Qwen2.5-32B shapes the
+// m-fastest runs already read the fewest rows.
 template <int WM, int WN, int BK, int S, int WGM = 2, int WGN = 4>
 int launch_fp8_wide(const Fp8Args &g, hipStream_t st) {
     using T = WideTile<WM, WN, BK, WGM, WGN>;
