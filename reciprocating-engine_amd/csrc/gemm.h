@@ -40,7 +40,7 @@ int launch_gemv_norm_rope(const float *x, const float *gamma, float eps, const u
 // 2 <= M <= 16 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
 int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed);
-// 16 < M <= 64 bf16 activation rows, K % 128 == 0 (csrc/skinny.hip).
+// Up to 64 bf16 activation rows on skinny_wide (16 < M, or K % 128 != 0), K % 16 == 0 (csrc/skinny.hip).
 int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed);
 // More than 64 activation rows, K % 64 == 0, on whole output tiles

@@ -843,12 +843,14 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     if (M > 64 && K % 64 == 0 && w8a16_tiles_take(M, N, K))
         return launch_w8a16_tiles(x, codes, scales, M, N, K, F, y, st, fixed);
     if (M > 4 && K % 128 != 0) {
-        // The MFMA kernel walks K in 128-code chunks; other widths take the
-        // GEMV kernel four activation rows at a time.
-        for (uint32_t mb = 0; mb < M; mb += 4) {
-            const uint32_t mt = M - mb < 4 ? M - mb : 4;
-            const int rc = launch_w8a16_t<F>(x + (size_t)mb * K, codes, scales, mt, N, K,
-                                             y + (size_t)mb * N, st, fixed);
+        // K not a multiple of the 128-code chunk: skinny_wide (its last chunk
+        // short, zero-padded in registers) on up to 64 activation rows at a
+        // time, each code read once per 64 rows (the GEMV would read it once
+        // per 4).
+        for (uint32_t mb = 0; mb < M; mb += 64) {
+            const uint32_t mt = M - mb < 64 ? M - mb : 64;
+            const int rc = launch_skinny_wide(x + (size_t)mb * K, codes, scales, mt, N, K, F, y + (size_t)mb * N, st,
+                                              fixed);
             if (rc) return rc;
         }
         return RENG_HIP_OK;

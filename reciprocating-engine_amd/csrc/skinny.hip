@@ -492,13 +492,18 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
         if (tile >= tiles) return;   // the XCD-major grid's padding
     }
     const uint32_t n0 = tile * R;
-    const uint32_t chunks = K / CHUNK;
+    // K need not be a multiple of the 128-code chunk (a multiple of 16): the
+    // last chunk then holds kr < 128 codes. Its copies past K read the row's
+    // first piece instead (in bounds), and its compute zeroes both operands
+    // past K, so the padding adds exact zeros.
+    const uint32_t chunks = (K + CHUNK - 1) / CHUNK, kr = K - (chunks - 1) * CHUNK;
     const uint32_t kc0 = split * cps, kc1 = kc0 + cps < chunks ? kc0 + cps : chunks;
     const uint32_t nst = kc1 - kc0;
+    const uint32_t st_ragged = kr < CHUNK && kc1 == chunks ? nst - 1 : 0xffffffffu;   // stage of the short chunk
 
     // This wave's copies q = wave + 4 c: q < WC a code copy, else activation copy q - WC.
     const uint8_t *src[C];
-    uint32_t dst[C], unit[C];
+    uint32_t dst[C], unit[C], back[C], past = 0;   // past bit c: copy c's piece lies past K in the short chunk
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const int q = wave + NWV * c;
@@ -509,6 +514,8 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
             src[c] = codes + (size_t)n * K + (size_t)kc0 * CHUNK + p * 16;
             dst[c] = q * 1024;
             unit[c] = 1;
+            back[c] = kc0 * CHUNK + p * 16;   // src[c] - back[c]: the row's first byte
+            past |= (16 * p >= kr ? 1u : 0u) << c;
         } else {
             const int qa = q - WC;
             const uint32_t row = qa * 4 + lane / 16, p = (lane % 16) ^ (row & 15);
@@ -516,14 +523,20 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
             src[c] = reinterpret_cast<const uint8_t *>(x + (size_t)m * K + (size_t)kc0 * CHUNK + p * 8);
             dst[c] = WB + qa * 1024;
             unit[c] = 2;
+            back[c] = (kc0 * CHUNK + p * 8) * 2;
+            past |= (8 * p >= kr ? 1u : 0u) << c;
         }
     }
     auto copies = [&](uint32_t st) {
         uint8_t *slot = lds + (st % S) * SLOT;
+        const bool short_chunk = st == st_ragged;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            if (unit[c] == 1) copy16_nt(src[c] + (size_t)st * BK, slot + dst[c]);
-            else copy16(src[c] + (size_t)st * BK * 2, slot + dst[c]);
+            // A piece past K in the short chunk reads the row's first piece
+            // instead (in bounds; zeroed in the compute).
+            const uint8_t *from = short_chunk && ((past >> c) & 1) ? src[c] - back[c] : src[c] + (size_t)st * BK * unit[c];
+            if (unit[c] == 1) copy16_nt(from, slot + dst[c]);
+            else copy16(from, slot + dst[c]);
         }
     };
 
@@ -531,7 +544,11 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
 #pragma unroll
     for (int f = 0; f < TPW * MTW; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](uint32_t st) {
+    // Lane l's k-step j of a chunk takes codes and activation [kb, kb + 8),
+    // kb = 16 (l / 16) + 8 (j % 2) + 64 (j / 2); in the short chunk those past
+    // K are zeroed (kr is a multiple of 16, so a run of 8 is all in or all out).
+    auto compute = [&](uint32_t st, auto short_c) {
+        constexpr bool SHORT = decltype(short_c)::value;
         const uint8_t *slot = lds + (st % S) * SLOT;
         u32x4 w[TPW][2];
 #pragma unroll
@@ -552,6 +569,9 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
             for (int j = 0; j < 4; ++j) {
                 const uint32_t p = 2 * g + (j & 1) + 8 * (j >> 1);
                 a[u][j] = *reinterpret_cast<const u32x4 *>(arow + ((p ^ (am & 15)) * 16));
+                if constexpr (SHORT) {
+                    if (8 * p >= kr) a[u][j] = u32x4{0u, 0u, 0u, 0u};
+                }
             }
         }
 #pragma unroll
@@ -559,7 +579,10 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
 #pragma unroll
             for (int t = 0; t < TPW; ++t) {
                 const u32x4 &q = w[t][j >> 1];
-                const bf16x8 wa = (j & 1) ? dec8<F>(q.z, q.w) : dec8<F>(q.x, q.y);
+                bf16x8 wa = (j & 1) ? dec8<F>(q.z, q.w) : dec8<F>(q.x, q.y);
+                if constexpr (SHORT) {
+                    if (16 * g + 8 * (j & 1) + 64 * (j >> 1) >= kr) wa = bf16x8{};
+                }
 #pragma unroll
                 for (int u = 0; u < MTW; ++u) {
                     if (wm + WMC * u >= MT) break;
@@ -590,7 +613,8 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
         wait_lgkm0();
         lds_barrier();   // everyone's copies of st landed; slot (st - 1) % S has been read
         if (st + S - 1 < nst) copies(st + S - 1);
-        compute(st);
+        if (st == st_ragged) compute(st, std::true_type{});
+        else compute(st, std::false_type{});
     }
 
     if (splits > 1 && !merge_splits<TPW * MTW, COH, NWV>(acc, part, part_bytes, cnt, tile, split, splits, &last_flag))
@@ -755,7 +779,7 @@ struct WidePlan {
 // round, with at least 4 chunks (512 codes) per split.
 WidePlan wide_plan(uint32_t mt, uint32_t N, uint32_t K) {
     const uint32_t cus = (uint32_t)device_props().cus, per_xcd = cus / 8 > 0 ? cus / 8 : 1;
-    const uint32_t chunks = K / CHUNK, max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
+    const uint32_t chunks = (K + CHUNK - 1) / CHUNK, max_splits = chunks / 4 > 1 ? chunks / 4 : 1;
     auto tiles_of = [&](uint32_t R) { return (N + R - 1) / R; };
     auto splits_of = [&](uint32_t R) {
         const uint32_t t = tiles_of(R);
@@ -927,7 +951,8 @@ int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *sca
     return launch_ma<RENG_HIP_E5M2, 16>(x, codes, scales, M, N, K, y, st);
 }
 
-// 16 < M <= 64, K % 128 == 0.
+// 1 <= M <= 64 on skinny_wide (16 < M, or any M whose K is not a multiple of
+// 128: its last chunk is short), K % 16 == 0.
 int launch_skinny_wide(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M, uint32_t N,
                        uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     using namespace skinny;

@@ -206,6 +206,49 @@ def test_skinny_gemm_ragged_batches(R, M):
     check_w8a16(R, rng, M, 48, 4096, E5M2)
 
 
+# K not a multiple of the 128-code chunk, M > 4: skinny_wide with a short last
+# chunk (16 to 112 codes), zero-padded in registers, on 1 to 64 activation rows
+# per launch (M = 100: a 64-row and a 36-row launch; the tiled kernel wants
+# K % 64 == 0). Shapes with K splits (the short chunk in the last split), one
+# chunk in all (K = 48, 80), one weight row tile, N % 4 != 0 and long rows.
+@pytest.mark.parametrize("M", [5, 8, 17, 40, 64, 100])
+@pytest.mark.parametrize("N,K", [(512, 3632), (1000, 1008), (77, 4000), (300, 5200), (64, 48), (17, 80),
+                                 (130, 18960)])
+def test_skinny_wide_short_last_chunk(R, M, N, K):
+    rng = np.random.default_rng(4000 * M + N + K)
+    fmt = E4M3 if (M + K // 16) % 2 else E5M2
+    check_w8a16(R, rng, M, N, K, fmt, sample_cols=None if M * N * K <= 64 * 1024 * 4096 else 256)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 512, 3632), (8, 1000, 1008), (33, 130, 18960)])
+def test_short_last_chunk_is_deterministic(R, M, N, K):
+    """The short chunk's padding adds exact zeros wherever it falls: repeated
+    calls give the same bits, equal to the product over K zero-padded to a
+    whole chunk (the same codes and activation with 128 - K % 128 zero columns
+    appended)."""
+    rng = np.random.default_rng(M * N + K)
+    q = quantized_weight(rng, N, K, E4M3)
+    xh = bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    x, c, s = dev(xh.ravel()), dev(q.codes), dev(q.scales)
+    first = R.gemm_w8a16(x, c, s, M, N, K, E4M3).clone()
+    for _ in range(2):
+        assert torch.equal(R.gemm_w8a16(x, c, s, M, N, K, E4M3), first)
+    Kp = (K + 127) // 128 * 128
+    cp = np.zeros((N, Kp), dtype=np.uint8)
+    cp[:, :K] = q.codes.reshape(N, K)
+    xp = np.zeros((M, Kp), dtype=np.uint16)
+    xp[:, :K] = xh.reshape(M, K)
+    padded = R.gemm_w8a16(dev(xp.ravel()), dev(cp.ravel()), s, M, N, Kp, E4M3)
+    torch.cuda.synchronize()
+    if M > 16:
+        # The same kernel and plan over whole chunks (the same chunk count):
+        # the padding's products are the same zeros, so the same bits.
+        assert torch.equal(first, padded)
+    else:
+        # Whole chunks at M <= 16 take the 16-row kernels: another order of sums.
+        assert O.rel_l2(bf16_out(first).ravel(), bf16_out(padded).ravel()) < 4e-3
+
+
 # 4 < M <= 16 (skinny_rows): every block shape the launcher picks (16, 32, 64,
 # 80 or 128 rows per block by N; the 80-row form holds the activation in LDS
 # for M <= 8 and K <= 4096: N = 20000, and 18950 at that K limit), K runs with

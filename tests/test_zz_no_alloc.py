@@ -52,6 +52,7 @@ def call(R, name, x, codes, scales, M, N, K, fmt):
     ((130, 2048, 1024), (65, 700, 512)),      # M > 64: 64-row tiles share the scratch in stream order
     ((8, 18944, 3584), (1, 4096, 4096)),      # no split: skinny_rows, then the GEMV
     ((256, 2048, 8192), (100, 1000, 8192)),   # stream-K partials and counters, then a smaller stream-K plan
+    ((64, 512, 3632), (9, 1000, 1008)),       # K % 128 != 0: a short last chunk, K splits both times
 ])
 def test_noalloc_matches_the_allocating_entry_twice(R, first, second):
     rng = np.random.default_rng(sum(first) + sum(second))
