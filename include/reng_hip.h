@@ -156,7 +156,7 @@ RENG_HIP_API int reng_hip_gemm_w8a16(const uint16_t *x, const uint8_t *codes, co
  * It is for callers that cannot allocate device memory during the call - code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc. Same arguments, kernels and results (bit for bit) as
- * reng_hip_gemm_w8a16; the split-K partials of 16 < M <= 64 products (and of
+ * reng_hip_gemm_w8a16; the split-K partials of 2 <= M <= 64 products (and of
  * each 64-row tile of a larger M) and the stream-K partials of long-K M > 64
  * products go to a static 32 MiB array in device memory, and the stream-K
  * tile counters to a static array of 4096 counters, that the library holds on
