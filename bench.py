@@ -257,6 +257,19 @@ def graph_time(torch, fn, n_launch, reps=3):
     return best
 
 
+def cool_down(torch, secs=20.0):
+    """Idle the device before the GEMV / GEMM timings. Right after the
+    Qwen2.5-32B quantize (minutes of full-rate HBM traffic) every launch over
+    HBM runs 3-5% slower for a while — measured on MI355X in one process: the
+    read yardstick over [4096, 14336] x 10 copies 9.55 us fresh, 9.83 after that
+    part, 9.85 after torch.cuda.empty_cache(), 9.52 after 20 s idle (the GEMV
+    10.40 / 10.98 / 10.96 / 10.36 us) — so the timings that follow are of the
+    device's steady state, the same for each kernel and its yardstick."""
+    torch.cuda.synchronize()
+    time.sleep(secs)
+    return secs
+
+
 def settle(torch, R, bufs, nbytes, secs=0.03):
     """Keep the device reading buffers for `secs` (back-to-back launches
     replayed from a hipGraph) before timing anything over them. After the
@@ -860,6 +873,7 @@ def main():
         extras["quantize_host_llama8b"] = bench_host_quantize(torch, R)
         log("host-pointer quantize:", extras["quantize_host_llama8b"])
         extras["f32_2048x2048_quantize"] = bench_f32_quantize(torch, R, gen, cpu=not args.no_cpu)
+        extras["cool_down_s"] = cool_down(torch)
         extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
                                      bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True)]
         extras["launch_floor"] = launch_floor(torch, R)
