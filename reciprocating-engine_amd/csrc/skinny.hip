@@ -461,7 +461,7 @@ __device__ __forceinline__ bool merge_splits(f32x4 (&frag)[NF], float *part, uin
     return true;
 }
 
-template <int F, int MT, int NTW, int S, int COH, int NWV>
+template <int F, int MT, int NTW, int S, int COH, int NWV, bool RAG>
 __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes,
                                                    const float *__restrict__ scales, uint32_t M, uint32_t N,
                                                    uint32_t K, uint32_t tiles, uint32_t splits, uint32_t cps,
@@ -492,14 +492,15 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
         if (tile >= tiles) return;   // the XCD-major grid's padding
     }
     const uint32_t n0 = tile * R;
-    // K need not be a multiple of the 128-code chunk (a multiple of 16): the
-    // last chunk then holds kr < 128 codes. Its copies past K read the row's
+    // RAG: K is not a multiple of the 128-code chunk (a multiple of 16), and
+    // the last chunk holds kr < 128 codes. Its copies past K read the row's
     // first piece instead (in bounds), and its compute zeroes both operands
-    // past K, so the padding adds exact zeros.
+    // past K, so the padding adds exact zeros. (A template argument: the
+    // checks cost the whole-chunk products 5% on small shapes.)
     const uint32_t chunks = (K + CHUNK - 1) / CHUNK, kr = K - (chunks - 1) * CHUNK;
     const uint32_t kc0 = split * cps, kc1 = kc0 + cps < chunks ? kc0 + cps : chunks;
     const uint32_t nst = kc1 - kc0;
-    const uint32_t st_ragged = kr < CHUNK && kc1 == chunks ? nst - 1 : 0xffffffffu;   // stage of the short chunk
+    const uint32_t st_ragged = RAG && kc1 == chunks ? nst - 1 : 0xffffffffu;   // stage of the short chunk
 
     // This wave's copies q = wave + 4 c: q < WC a code copy, else activation copy q - WC.
     const uint8_t *src[C];
@@ -529,14 +530,23 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
     }
     auto copies = [&](uint32_t st) {
         uint8_t *slot = lds + (st % S) * SLOT;
-        const bool short_chunk = st == st_ragged;
+        if constexpr (RAG) {
+            const bool short_chunk = st == st_ragged;
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-            // A piece past K in the short chunk reads the row's first piece
-            // instead (in bounds; zeroed in the compute).
-            const uint8_t *from = short_chunk && ((past >> c) & 1) ? src[c] - back[c] : src[c] + (size_t)st * BK * unit[c];
-            if (unit[c] == 1) copy16_nt(from, slot + dst[c]);
-            else copy16(from, slot + dst[c]);
+            for (int c = 0; c < C; ++c) {
+                // A piece past K in the short chunk reads the row's first piece
+                // instead (in bounds; zeroed in the compute).
+                const uint8_t *from =
+                    short_chunk && ((past >> c) & 1) ? src[c] - back[c] : src[c] + (size_t)st * BK * unit[c];
+                if (unit[c] == 1) copy16_nt(from, slot + dst[c]);
+                else copy16(from, slot + dst[c]);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                if (unit[c] == 1) copy16_nt(src[c] + (size_t)st * BK, slot + dst[c]);
+                else copy16(src[c] + (size_t)st * BK * 2, slot + dst[c]);
+            }
         }
     };
 
@@ -613,7 +623,7 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
         wait_lgkm0();
         lds_barrier();   // everyone's copies of st landed; slot (st - 1) % S has been read
         if (st + S - 1 < nst) copies(st + S - 1);
-        if (st == st_ragged) compute(st, std::true_type{});
+        if (RAG && st == st_ragged) compute(st, std::integral_constant<bool, RAG>{});
         else compute(st, std::false_type{});
     }
 
@@ -840,12 +850,16 @@ int launch_wide_cfg(const uint16_t *x, const uint8_t *codes, const float *scales
         coh = split_coherence(st, fixed == nullptr);
         grid = 8 * ((p.tiles + 7) / 8) * p.splits;
     }
-    if (coh)
-        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 1, NWV>), dim3(grid), dim3(64 * NWV), 0, st, x, codes, scales,
-                           M, N, K, p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
-    else
-        hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, 0, NWV>), dim3(grid), dim3(64 * NWV), 0, st, x, codes, scales,
-                           M, N, K, p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt);
+#define RENG_WIDE(C, RG)                                                                                        \
+    hipLaunchKernelGGL((skinny_wide<F, MT, NTW, S, C, NWV, RG>), dim3(grid), dim3(64 * NWV), 0, st, x, codes, scales, \
+                       M, N, K, p.tiles, p.splits, p.cps, y, part, (uint32_t)bytes, cnt)
+    const bool rag = K % CHUNK != 0;
+    if (coh) {
+        if (rag) RENG_WIDE(1, true); else RENG_WIDE(1, false);
+    } else {
+        if (rag) RENG_WIDE(0, true); else RENG_WIDE(0, false);
+    }
+#undef RENG_WIDE
     return check_launch("skinny_wide");
 }
 
