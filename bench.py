@@ -270,14 +270,26 @@ def cool_down(torch, secs=20.0):
     return secs
 
 
-def settle(torch, R, bufs, nbytes, secs=0.03):
+SETTLE_S = 0.03   # bench.py --settle-ms
+
+
+def set_settle(secs):
+    global SETTLE_S
+    SETTLE_S = secs
+
+
+def settle(torch, R, bufs, nbytes, secs=None):
     """Keep the device reading buffers for `secs` (back-to-back launches
     replayed from a hipGraph) before timing anything over them. After the
     weights are written and the device idles for a moment, launches over them
     run 3-8% slower for the first ~15 ms of continuous work (measured on MI355X
     over [4096, 14336] x 10 copies: the read yardstick 9.84 against 9.58 us, the
     GEMV 11.1 against 10.33); launches issued one by one from the host (idle
-    gaps between them) did not end it."""
+    gaps between them) did not end it. Counter passes of rocprofv3 serialize
+    every launch, so they run with --settle-ms 0 (no warm-up reads)."""
+    secs = SETTLE_S if secs is None else secs
+    if secs <= 0:
+        return
     sink = torch.empty(R.stream_read_sink_bytes(), dtype=torch.uint8, device="cuda")
     n = nbytes - nbytes % 1024
     torch.cuda.synchronize()
@@ -772,10 +784,13 @@ def main():
                     choices=["all", "quantize", "gemv", "skinny", "tiles", "prefill", "f32", "decode", "qwen32b",
                              "host"],
                     help="run one part only (for profiling); the JSON line is printed for 'all' and 'quantize'")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_S * 1e3,
+                    help="back-to-back reads of each product's weights before it is timed (0 for counter passes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy 1 GiB device-to-device three times first: a kernel of known traffic that "
                          "scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    set_settle(args.settle_ms / 1e3)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this path runs on a single MI355X and has no multi-GPU "
