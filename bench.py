@@ -258,13 +258,17 @@ def graph_time(torch, fn, n_launch, reps=3):
 
 
 def cool_down(torch, secs=20.0):
-    """Idle the device before the GEMV / GEMM timings. Right after the
+    """Idle the device before a group of GEMV / GEMM timings. Right after the
     Qwen2.5-32B quantize (minutes of full-rate HBM traffic) every launch over
     HBM runs 3-5% slower for a while — measured on MI355X in one process: the
     read yardstick over [4096, 14336] x 10 copies 9.55 us fresh, 9.83 after that
     part, 9.85 after torch.cuda.empty_cache(), 9.52 after 20 s idle (the GEMV
-    10.40 / 10.98 / 10.96 / 10.36 us) — so the timings that follow are of the
-    device's steady state, the same for each kernel and its yardstick."""
+    10.40 / 10.98 / 10.96 / 10.36 us). Later groups follow seconds of their own
+    full-rate work, and the MFMA kernels among them lose 5-10% there while
+    their read yardsticks do not (skinny M = 64 gate/up 24.8 against 22.5 us,
+    the read 10.7-10.8 us both), so each group starts after 10 s idle. The
+    timings are of the device's steady state, the same for each kernel and
+    its yardstick."""
     torch.cuda.synchronize()
     time.sleep(secs)
     return secs
@@ -895,6 +899,7 @@ def main():
         extras["read_fit"] = read_fit(torch, R)
         log("gemv b1:", extras["gemv_b1_llama8b"], "launch floor:", extras["launch_floor"],
             "read fit:", extras["read_fit"])
+        extras["cool_down_s"] += cool_down(torch, 10.0)
         sk = []
         for M in (8, 64):
             for _, N, K in QWEN_7B:
@@ -902,8 +907,10 @@ def main():
         extras["skinny_qwen7b"] = sk
         log("skinny:", sk)
         torch.cuda.empty_cache()
+        extras["cool_down_s"] += cool_down(torch, 10.0)
         extras["w8a16_tiles"] = bench_w8a16_tiles(torch, R, gen)
         log("w8a16 tiles:", extras["w8a16_tiles"])
+        extras["cool_down_s"] += cool_down(torch, 10.0)
         extras["prefill_fp8_m1024_qwen32b"] = [bench_fp8_gemm(torch, R, gen, 1024, N, K)
                                                for N, K in ((5120, 5120), (1024, 5120), (27648, 5120),
                                                             (5120, 27648))]
