@@ -502,7 +502,7 @@ __global__ __launch_bounds__(64 * NWV) void skinny_wide(const uint16_t *__restri
     const uint32_t nst = kc1 - kc0;
     const uint32_t st_ragged = RAG && kc1 == chunks ? nst - 1 : 0xffffffffu;   // stage of the short chunk
 
-    // This wave's copies q = wave + 4 c: q < WC a code copy, else activation copy q - WC.
+    // This wave's copies q = wave + NWV c: q < WC a code copy, else activation copy q - WC.
     const uint8_t *src[C];
     uint32_t dst[C], unit[C], back[C], past = 0;   // past bit c: copy c's piece lies past K in the short chunk
 #pragma unroll
