@@ -406,13 +406,19 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 // their epilogue. A ragged last chunk (K % 1024 != 0) masks the lanes past K.
 constexpr int GEMV_WINDOW = 10;
 
-template <int F, int CPR, int WPB>
+//
+// EPI_RESID (the decode step's projections that feed the residual stream)
+// writes f32 yres[n] = res[n] + bf16(y[n]) instead of y: gemv_w8a16's residual
+// epilogue on the same row sums, so the same bits.
+template <int F, int CPR, int WPB, int EPI = EPI_PLAIN>
 // (No __restrict__ on the inputs: loads through a restrict pointer to const may
 // be treated as invariant and moved across the compiler barriers that fix the
 // issue order.)
 __global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *x, const uint8_t *codes,
                                                       const float *scales, uint32_t N, uint32_t K,
-                                                      uint16_t *__restrict__ y) {
+                                                      uint16_t *__restrict__ y, const float *res,
+                                                      float *__restrict__ yres) {
+    static_assert(EPI == EPI_PLAIN || EPI == EPI_RESID, "plain or residual rows");
     constexpr uint32_t XMAX = CPR * 128;                             // 16-byte activation pieces at most
     constexpr uint32_t XPT = (XMAX + 64 * WPB - 1) / (64 * WPB);     // pieces per thread
     __shared__ __attribute__((aligned(16))) u32x4 xs[XMAX];
@@ -472,7 +478,11 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *x, const u
         a1 = dot2(wv[7], xb.w, a1);
     }
     const float t = wave_sum_dpp(a0 + a1);
-    if (lane == 0 && n < N) y[n] = (uint16_t)f32_to_bf16_bits(t * sv);
+    if (lane == 0 && n < N) {
+        const uint32_t b = f32_to_bf16_bits(t * sv);
+        if constexpr (EPI == EPI_RESID) yres[n] = res[n] + __uint_as_float(b << 16);
+        else y[n] = (uint16_t)b;
+    }
 }
 
 // ------------------------------------------------------------------ read yardstick
@@ -784,12 +794,6 @@ int launch_gemv_norm(const float *x, const float *gamma, float eps, const uint8_
                   : launch_gemv_norm_t<RENG_HIP_E5M2, EPI_PLAIN>(x, gamma, eps, codes, scales, N, K, y, st);
 }
 
-int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
-                         int format, const float *res, float *y, hipStream_t st) {
-    return format == RENG_HIP_E4M3
-               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, nullptr, 0.0f, st)
-               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, nullptr, 0.0f, st);
-}
 
 int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                        int format, uint16_t *y, hipStream_t st) {
@@ -804,23 +808,25 @@ int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *sca
 // when there are more than 16 rows per CU, else 8-wave blocks (fewer copies
 // of a long activation per CU): [14336, 4096] 10.12 us with 4-wave blocks
 // against 10.25 with 8, [4096, 4096] 4.54 against 4.46.
-template <int F, int CPR>
+template <int F, int CPR, int EPI>
 int launch_gemv_rows_c(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
-                       uint16_t *y, hipStream_t st) {
+                       uint16_t *y, const float *res, float *yres, hipStream_t st) {
     if (CPR <= 8 && N > (uint32_t)device_props().cus * 16)
-        hipLaunchKernelGGL((gemv_rows<F, CPR, 4>), dim3((N + 3) / 4), dim3(256), 0, st, x, codes, scales, N, K, y);
+        hipLaunchKernelGGL((gemv_rows<F, CPR, 4, EPI>), dim3((N + 3) / 4), dim3(256), 0, st, x, codes, scales, N, K, y,
+                           res, yres);
     else
-        hipLaunchKernelGGL((gemv_rows<F, CPR, 8>), dim3((N + 7) / 8), dim3(512), 0, st, x, codes, scales, N, K, y);
-    return check_launch("gemv_rows");
+        hipLaunchKernelGGL((gemv_rows<F, CPR, 8, EPI>), dim3((N + 7) / 8), dim3(512), 0, st, x, codes, scales, N, K, y,
+                           res, yres);
+    return check_launch(EPI == EPI_RESID ? "gemv_rows (residual)" : "gemv_rows");
 }
 
 // Rows of 2..16 KB (1024 < K <= 16384); the caller sends the rest to gemv_w8a16.
-template <int F>
+template <int F, int EPI = EPI_PLAIN>
 int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
-                     uint16_t *y, hipStream_t st) {
+                     uint16_t *y, hipStream_t st, const float *res = nullptr, float *yres = nullptr) {
     switch ((K + 1023) / 1024) {
 #define RENG_ROWS(C) \
-    case C: return launch_gemv_rows_c<F, C>(x, codes, scales, N, K, y, st);
+    case C: return launch_gemv_rows_c<F, C, EPI>(x, codes, scales, N, K, y, res, yres, st);
         RENG_ROWS(2) RENG_ROWS(3) RENG_ROWS(4) RENG_ROWS(5) RENG_ROWS(6) RENG_ROWS(7) RENG_ROWS(8) RENG_ROWS(9)
         RENG_ROWS(10) RENG_ROWS(11) RENG_ROWS(12) RENG_ROWS(13) RENG_ROWS(14) RENG_ROWS(15) RENG_ROWS(16)
 #undef RENG_ROWS
@@ -828,6 +834,20 @@ int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scale
             set_error("gemv_rows: K = %u outside 1025..16384", K);
             return RENG_HIP_EINVAL;
     }
+}
+
+int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
+                         int format, const float *res, float *y, hipStream_t st) {
+    // Rows of 2..16 KB on gemv_rows (the decode step's o and down projections:
+    // [4096, 4096] 5.07 -> 4.5 us, [4096, 14336] 11.6 -> 10.4 us on the same
+    // row sums), the rest on the strided walk.
+    if (K > 1024 && K <= 16384)
+        return format == RENG_HIP_E4M3
+                   ? launch_gemv_rows<RENG_HIP_E4M3, EPI_RESID>(x, codes, scales, N, K, nullptr, st, res, y)
+                   : launch_gemv_rows<RENG_HIP_E5M2, EPI_RESID>(x, codes, scales, N, K, nullptr, st, res, y);
+    return format == RENG_HIP_E4M3
+               ? launch_gemv_epi_t<RENG_HIP_E4M3, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, nullptr, 0.0f, st)
+               : launch_gemv_epi_t<RENG_HIP_E5M2, EPI_RESID>(x, codes, scales, N, K, nullptr, res, y, nullptr, 0.0f, st);
 }
 
 template <int F>
