@@ -1,6 +1,6 @@
 // gemm.hip - consumers of the quantizer's codes on CDNA4 (gfx950).
 //
-// 1. gemv_rows      (M = 1, 1024 < K <= 16384) and gemv_w8a16 (the other
+// 1. gemv_rows      (M = 1, 1024 < K <= 32768) and gemv_w8a16 (the other
 //                    M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
 //                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]); with
 //                    M = 1 gemv_w8a16 also has residual-add, SwiGLU-pair and
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16(const uint16_t *__restrict__ x
 
 // ------------------------------------------------------------------ GEMV, M = 1
 
-// One wave per output row; the row's CPR 1 KB chunks (K <= 16384) stream
+// One wave per output row; the row's CPR 1 KB chunks (K <= 32768) stream
 // through a window of GEMV_WINDOW chunks: the first min(CPR, GEMV_WINDOW) are
 // requested at the start, and chunk c + GEMV_WINDOW is requested just before
 // chunk c is consumed. In issue order: the row's scale, this thread's share of
@@ -811,16 +811,23 @@ int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *sca
 template <int F, int CPR, int EPI>
 int launch_gemv_rows_c(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                        uint16_t *y, const float *res, float *yres, hipStream_t st) {
-    if (CPR <= 8 && N > (uint32_t)device_props().cus * 16)
-        hipLaunchKernelGGL((gemv_rows<F, CPR, 4, EPI>), dim3((N + 3) / 4), dim3(256), 0, st, x, codes, scales, N, K, y,
-                           res, yres);
-    else
-        hipLaunchKernelGGL((gemv_rows<F, CPR, 8, EPI>), dim3((N + 7) / 8), dim3(512), 0, st, x, codes, scales, N, K, y,
-                           res, yres);
+    if constexpr (CPR <= 8) {
+        if (N > (uint32_t)device_props().cus * 16) {
+            hipLaunchKernelGGL((gemv_rows<F, CPR, 4, EPI>), dim3((N + 3) / 4), dim3(256), 0, st, x, codes, scales, N, K,
+                               y, res, yres);
+            return check_launch(EPI == EPI_RESID ? "gemv_rows (residual)" : "gemv_rows");
+        }
+    }
+    hipLaunchKernelGGL((gemv_rows<F, CPR, 8, EPI>), dim3((N + 7) / 8), dim3(512), 0, st, x, codes, scales, N, K, y,
+                       res, yres);
     return check_launch(EPI == EPI_RESID ? "gemv_rows (residual)" : "gemv_rows");
 }
 
-// Rows of 2..16 KB (1024 < K <= 16384); the caller sends the rest to gemv_w8a16.
+// Rows of 2..32 KB (1024 < K <= 32768: the activation's LDS copy is at most
+// 64 KB); the caller sends the rest to gemv_w8a16. Past 16 chunks the load
+// window is what keeps the rows in order: M = 1 [5120, 27648] 28.1 -> 23.2 us,
+// [3584, 19456] 13.4-14.0 -> 12.1 us against the strided walk (a plain read of
+// the codes 20.9 / 11.1 us).
 template <int F, int EPI = EPI_PLAIN>
 int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                      uint16_t *y, hipStream_t st, const float *res = nullptr, float *yres = nullptr) {
@@ -829,19 +836,22 @@ int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scale
     case C: return launch_gemv_rows_c<F, C, EPI>(x, codes, scales, N, K, y, res, yres, st);
         RENG_ROWS(2) RENG_ROWS(3) RENG_ROWS(4) RENG_ROWS(5) RENG_ROWS(6) RENG_ROWS(7) RENG_ROWS(8) RENG_ROWS(9)
         RENG_ROWS(10) RENG_ROWS(11) RENG_ROWS(12) RENG_ROWS(13) RENG_ROWS(14) RENG_ROWS(15) RENG_ROWS(16)
+        RENG_ROWS(17) RENG_ROWS(18) RENG_ROWS(19) RENG_ROWS(20) RENG_ROWS(21) RENG_ROWS(22) RENG_ROWS(23)
+        RENG_ROWS(24) RENG_ROWS(25) RENG_ROWS(26) RENG_ROWS(27) RENG_ROWS(28) RENG_ROWS(29) RENG_ROWS(30)
+        RENG_ROWS(31) RENG_ROWS(32)
 #undef RENG_ROWS
         default:
-            set_error("gemv_rows: K = %u outside 1025..16384", K);
+            set_error("gemv_rows: K = %u outside 1025..32768", K);
             return RENG_HIP_EINVAL;
     }
 }
 
 int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                          int format, const float *res, float *y, hipStream_t st) {
-    // Rows of 2..16 KB on gemv_rows (the decode step's o and down projections:
+    // Rows of 2..32 KB on gemv_rows (the decode step's o and down projections:
     // [4096, 4096] 5.07 -> 4.5 us, [4096, 14336] 11.6 -> 10.4 us on the same
     // row sums), the rest on the strided walk.
-    if (K > 1024 && K <= 16384)
+    if (K > 1024 && K <= 32768)
         return format == RENG_HIP_E4M3
                    ? launch_gemv_rows<RENG_HIP_E4M3, EPI_RESID>(x, codes, scales, N, K, nullptr, st, res, y)
                    : launch_gemv_rows<RENG_HIP_E5M2, EPI_RESID>(x, codes, scales, N, K, nullptr, st, res, y);
@@ -853,9 +863,9 @@ int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *s
 template <int F>
 int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t M,
                    uint32_t N, uint32_t K, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
-    // One activation row of 1 to 16 KB: a wave per row with the whole row in
-    // flight; x and codes are 16-byte aligned (checked by the entry point).
-    if (M == 1 && K > 1024 && K <= 16384)
+    // One activation row of 1 to 32 KB: a wave per row, its chunks through a
+    // load window; x and codes are 16-byte aligned (checked by the entry point).
+    if (M == 1 && K > 1024 && K <= 32768)
         return launch_gemv_rows<F>(x, codes, scales, N, K, y, st);
     // More than 64 rows: output tiles on the bf16 MFMA, each code tile read
     // once per 64-256 activation rows (the 64-row loop below re-reads every

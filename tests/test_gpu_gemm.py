@@ -144,13 +144,14 @@ def test_gemv_batch1_llama_8b_shapes(R, fmt, shape):
 
 
 @pytest.mark.parametrize("N,K", [(1, 16), (7, 1040), (1000, 3584), (7169, 18944), (300, 32768), (64, 33792),
-                                 (20000, 512), (129, 14336), (333, 15008), (77, 16384), (5, 11264)])
+                                 (20000, 512), (129, 14336), (333, 15008), (77, 16384), (5, 11264),
+                                 (517, 27648), (9, 20000), (1031, 16400)])
 def test_gemv_batch1_contiguous_rows(R, N, K):
     """M = 1 on the contiguous-rows GEMV: ragged last chunks (K % 1024 != 0),
-    fewer rows than waves, a row count that leaves the last wave short, the
-    64 KB activation limit and one past it (the row-strided GEMV then), rows
-    longer than the 10-chunk load window (11 to 16 chunks, one of them ragged),
-    both formats, with and without the scale operand."""
+    fewer rows than waves, a row count that leaves the last wave short, rows
+    longer than the 10-chunk load window (11 to 32 chunks, ragged among them),
+    the 32-chunk limit (a 64 KB activation copy in LDS) and one past it (the
+    row-strided GEMV then), both formats, with and without the scale operand."""
     rng = np.random.default_rng(N + K)
     check_w8a16(R, rng, 1, N, K, E4M3 if N % 2 else E5M2)
     q = quantized_weight(rng, N, K, E4M3)
