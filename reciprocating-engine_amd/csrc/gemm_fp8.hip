@@ -316,7 +316,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_fp8_wide(const uint8_t *_
                                                                 const float *__restrict__ sb, uint32_t nsb, uint32_t M,
                                                                 uint32_t N, uint32_t K, uint32_t tiles_m,
                                                                 uint32_t tiles, uint16_t *__restrict__ out,
-                                                                uint32_t mapm) {
+                                                                uint32_t ldo, uint32_t mapm) {
     using T = WideTile<WM, WN, BKW, WGM, WGN>;
     constexpr int BM = T::BM, BN = T::BN, BK = T::BK, CH = T::CH, ROWS = T::ROWS, KS = BK / FK, NT = 64 * T::NW;
     static_assert(S >= 2, "at least double-buffered");
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_fp8_wide(const uint8_t *_
     for (int p = 0; p < BM * CC / NT; ++p) {
         const uint32_t i = p * NT + te, r = i / CC, c = i % CC;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + slot(r, c) * 16);
-        *reinterpret_cast<u32x4 *>(out + (size_t)(m0 + r) * N + n0 + 8 * c) = v;
+        *reinterpret_cast<u32x4 *>(out + (size_t)(m0 + r) * ldo + n0 + 8 * c) = v;
     }
 }
 
@@ -542,20 +542,77 @@ WideCand wide_cand(const Fp8Args &g, float c0, float c1) {
 // covers all, plus 2 n-tiles) blocks of 4 x 8 read 768 operand rows per XCD
 // instead of 1152: 15.0 -> 14.3-14.5 us. On the larger Qwen2.5-32B shapes the
 // m-fastest runs already read the fewest rows.
+//
+// ldo is the output's row stride in elements (0: N); a launch over a column
+// range of a wider output passes the whole output's N.
 template <int WM, int WN, int BK, int S, int WGM = 2, int WGN = 4>
-int launch_fp8_wide(const Fp8Args &g, hipStream_t st) {
+int launch_fp8_wide(const Fp8Args &g, hipStream_t st, uint32_t ldo = 0) {
     using T = WideTile<WM, WN, BK, WGM, WGN>;
     const uint32_t tiles_m = g.M / T::BM, tiles = tiles_m * (g.N / T::BN);
     const uint32_t mapm = wide_mapm(tiles_m, g.N / T::BN, T::BM, T::BN);
+    const uint32_t ld = ldo ? ldo : g.N;
 #define RENG_FP8_WIDE(A, B)                                                                                      \
     hipLaunchKernelGGL((gemm_fp8_wide<A, B, WM, WN, BK, S, WGM, WGN>), dim3(tiles), dim3(64 * T::NW), 0, st, g.a, g.sa, \
-                       g.nsa, g.b, g.sb, g.nsb, g.M, g.N, g.K, tiles_m, tiles, g.out, mapm)
+                       g.nsa, g.b, g.sb, g.nsb, g.M, g.N, g.K, tiles_m, tiles, g.out, ld, mapm)
     if (g.fa == RENG_HIP_E4M3 && g.fb == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 0);
     else if (g.fa == RENG_HIP_E4M3) RENG_FP8_WIDE(0, 1);
     else if (g.fb == RENG_HIP_E4M3) RENG_FP8_WIDE(1, 0);
     else RENG_FP8_WIDE(1, 1);
 #undef RENG_FP8_WIDE
     return check_launch("gemm_fp8_wide");
+}
+
+// The columns [n0, n0 + n) of a product as a product of its own: the codes and
+// per-channel scales of those weight rows, the output's columns from n0 (the
+// launch writes them with the whole output's row stride).
+inline Fp8Args column_range(const Fp8Args &g, uint32_t n0, uint32_t n) {
+    Fp8Args r = g;
+    r.b = g.b + (size_t)n0 * g.K;
+    if (g.nsb > 1) r.sb = g.sb + n0, r.nsb = n;
+    r.N = n;
+    r.out = g.out + n0;
+    return r;
+}
+
+// A grid of 256 x 256 tiles that is not a whole number of rounds pays for its
+// last, partial round in full. The mixed plan runs whole rounds of 256 x 256
+// tiles over the leading n1 columns, then one round of 256 x 192 tiles over
+// the rest (a second launch): on [1024, 27648, 5120] 252 + 240 tiles instead of
+// 432 in two rounds. The narrower tile reads 0.875x the operand rows per output
+// and its round measured 0.82-0.85x as long, so the plan gains 2-3% there
+// (141-146 -> 138-141 us; K = 10240: 260-263 -> 253-254 us), not the 16% of a
+// tile-count model: these tiles' rounds take time in proportion to the operand
+// bytes they copy. (One launch holding both forms, the second's workgroups
+// dispatched as the first's finish, measured the same as two launches.)
+// n1 = 0: no plan. est uses the 256 x 192 form's (c0, c1) fitted to its
+// timings at K = 2560, 5120 and 10240.
+struct MixedPlan {
+    uint32_t n1;
+    float est;
+};
+
+inline MixedPlan mixed_plan(const Fp8Args &g, uint64_t cus, float c0a, float c1a, float c0b, float c1b) {
+    using TA = WideTile<4, 2, 128, 2, 4>;
+    using TB = WideTile<2, 3, 128, 4, 2>;
+    MixedPlan best{0, 0.0f};
+    if (g.M % TA::BM != 0 || g.N % 64 != 0 || g.K % TA::BK != 0) return best;
+    const uint64_t tiles_m = g.M / TA::BM, stages = g.K / TA::BK;
+    const uint64_t rounds_a = tiles_m * (g.N / TA::BN) / cus;   // whole rounds of the 256 x 256 tiles
+    for (uint64_t r = 1; r <= rounds_a; ++r) {
+        const uint64_t amax = r * cus / tiles_m;
+        for (uint64_t a = amax; a + 3 > amax && a > 0; --a) {
+            if (a * TA::BN >= g.N) continue;
+            const uint64_t rest = g.N - a * TA::BN;
+            if (rest % TB::BN != 0 || tiles_m * (rest / TB::BN) > cus) continue;
+            if (!wide_fits<4, 2, 128, 2, 4>(column_range(g, 0, (uint32_t)(a * TA::BN))) ||
+                !wide_fits<2, 3, 128, 4, 2>(column_range(g, (uint32_t)(a * TA::BN), (uint32_t)rest)))
+                continue;
+            const float est = (float)((tiles_m * a + cus - 1) / cus) * (c0a + c1a * (float)stages) +
+                              (c0b + c1b * (float)stages);
+            if (best.n1 == 0 || est < best.est) best = MixedPlan{(uint32_t)(a * TA::BN), est};
+        }
+    }
+    return best;
 }
 
 }  // namespace fp8gemm
@@ -587,6 +644,12 @@ int launch_fp8_gemm(const uint8_t *a, int fa, const float *sa, uint32_t nsa, con
         const uint64_t tiles = (uint64_t)(M / cands[i].bm) * (N / cands[i].bn);
         const float est = (float)((tiles + cus - 1) / cus) * (cands[i].c0 + cands[i].c1 * (float)(K / 128));
         if (pick < 0 || est < best) pick = i, best = est;
+    }
+    const MixedPlan mp = mixed_plan(g, cus, cands[0].c0, cands[0].c1, 8.2f, 1.353f);
+    if (mp.n1 != 0 && (pick < 0 || mp.est < best)) {
+        const int rc = launch_fp8_wide<4, 2, 128, 2>(column_range(g, 0, mp.n1), st, N);
+        if (rc != RENG_HIP_OK) return rc;
+        return launch_fp8_wide<2, 3, 128, 2, 4, 2>(column_range(g, mp.n1, N - mp.n1), st, N);
     }
     switch (pick) {
     case 0: return launch_fp8_wide<4, 2, 128, 2>(g, st);

@@ -488,11 +488,13 @@ def test_fp8_gemm_ragged_tiles(R, M, N, K):
 
 
 # Whole-tile shapes take the wide forms, one shape per tile the launcher's
-# cost model picks: 256 x 256 (1024 x 16384), 256 x 128 (512 x 16384),
-# 128 x 160 (1024 x 5120), 128 x 128 (1024 x 4096) and 64 x 64 (256 x 32768);
-# K of one to eight 128-code stages, every format pair and scale form.
+# cost model picks on a 256-CU MI355X: 256 x 256 (1024 x 16384), 256 x 128
+# (512 x 16384), 128 x 160 (1024 x 5120), 128 x 128 (1024 x 4096), 64 x 64
+# (256 x 32768), and the mixed grid (1024 x 27648: 252 tiles of 256 x 256 over
+# the first 16128 columns, 240 of 256 x 192 over the rest); K of one to eight
+# 128-code stages, every format pair and scale form.
 @pytest.mark.parametrize("M,N,K", [(1024, 16384, 256), (512, 16384, 384), (1024, 5120, 1024), (1024, 4096, 1024),
-                                   (256, 32768, 128)])
+                                   (256, 32768, 128), (1024, 27648, 256)])
 @pytest.mark.parametrize("fa,fb", [(E4M3, E4M3), (E5M2, E5M2), (E4M3, E5M2), (E5M2, E4M3)])
 def test_fp8_gemm_wide_tiles(R, M, N, K, fa, fb):
     rng = np.random.default_rng(M + N + K + 4 * fa + fb)
