@@ -774,7 +774,10 @@ struct WidePlan {
 // Rows per block first: for 16 < M <= 64 (mt >= 2), 64 on small matrices (the
 // partials of more splits cost more than the activation re-reads) or 32 where
 // 64-row blocks split as far as they go would keep under half the CUs busy
-// (Qwen2.5-7B kv [512, 3584] at M = 64: 8.84 -> 6.94 us); on large ones 128
+// (Qwen2.5-7B kv [512, 3584] at M = 64: 8.84 -> 6.94 us), or exactly half
+// with 32-row blocks split at most 8 ways (Llama-3.1-8B kv [1024, 4096] at
+// M = 64 8.07 -> 7.42 us, M = 32 6.55 -> 6.23 us; [2048, 2048] 7.50 -> 7.11
+// us; [512, 8192], 16 ways, stays at 64 rows: 9.10 against 9.37 us); on large ones 128
 // (half the activation bytes per code). With an even number of activation
 // tiles the 64- and 128-row blocks run 8 waves (two per SIMD, each issuing
 // half the copies and computing half the tiles): the copy stream is what
@@ -801,7 +804,8 @@ WidePlan wide_plan(uint32_t mt, uint32_t N, uint32_t K) {
     WidePlan p{2, 4, 4, 0, 1, chunks};
     if (mt >= 2) {
         if (small) {
-            if (2 * tiles_of(64) * max_splits < cus) p.ntw = 1;
+            const uint32_t half64 = 2 * tiles_of(64) * max_splits;
+            if (half64 < cus || (half64 == cus && splits_of(32) <= 8)) p.ntw = 1;
         } else if (mt % 2 == 0) {
             p.ntw = 4;
         } else {

@@ -280,11 +280,12 @@ def test_skinny_wide_block_shapes(R, M, N, K):
 
 # The K splits merged inside the launch: M <= 16 products on the split form
 # (K >= 8192; 8 < M <= 16 outside the band where 16-row tiles fill half to all
-# of the CUs), 16 < M <= 64 with 32-row blocks (few tiles), row tiles not a
-# multiple of the 8 XCDs (padding blocks in the XCD-major grid), a short last
+# of the CUs), 16 < M <= 64 with 32-row blocks (few tiles, and the tie where
+# 64-row blocks would fill exactly half the CUs: [1024, 4096]), row tiles not
+# a multiple of the 8 XCDs (padding blocks in the XCD-major grid), a short last
 # split, N % 4 != 0, one row tile in all, and 2 <= M <= 4 on long rows.
 @pytest.mark.parametrize("M", [2, 8, 12, 16, 24, 64])
-@pytest.mark.parametrize("N,K", [(512, 3584), (1000, 8192), (77, 9344), (3000, 2944), (200, 16384)])
+@pytest.mark.parametrize("N,K", [(512, 3584), (1000, 8192), (77, 9344), (3000, 2944), (200, 16384), (1024, 4096)])
 def test_split_merge_shapes(R, M, N, K):
     rng = np.random.default_rng(3000 * M + N + K)
     fmt = E4M3 if (M + K // 128) % 2 else E5M2
