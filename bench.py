@@ -15,7 +15,9 @@ quantize (64 layers, 31.2 G elements, layer 0 compared bit for bit with the
 oracle); the f32 [2048, 2048] quantize rotated over 32 copies (compared with the
 oracle); the fused dequant GEMV at batch 1 on the [14336, 4096] and
 [4096, 14336] shapes rotated past the Infinity Cache, next to a plain read of
-the same bytes (the one-launch read yardstick); the skinny GEMM at batch 8 and
+the same bytes (the one-launch read yardstick), and on the long rows of the
+Qwen2.5-7B and -32B down projections ([3584, 18944], [5120, 27648]); the
+skinny GEMM at batch 8 and
 64 on Qwen2.5-7B shapes; the M = 1024 fp8 x fp8 GEMM on Qwen2.5-32B shapes, each
 beside hipBLASLt (torch._scaled_mm) on the same codes; the fp8 decode step; the
 quantizer's stream yardstick (the same 2 bytes in and 1 byte out per element
@@ -54,6 +56,8 @@ MALL_BYTES = MI355X.sram_bytes   # Infinity Cache: timed buffers rotate over mor
 LLAMA_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
             ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
 QWEN_7B = [("q/o", 3584, 3584), ("k/v", 512, 3584), ("gate/up", 18944, 3584), ("down", 3584, 18944)]
+# Batch-1 GEMV rows longer than 16 KB: the Qwen2.5-7B and Qwen2.5-32B down projections [N, K].
+LONG_ROWS = [(3584, 18944), (5120, 27648)]
 QWEN_32B = [("q", 5120, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120, 5120),
             ("gate", 27648, 5120), ("up", 27648, 5120), ("down", 5120, 27648)]
 
@@ -822,6 +826,7 @@ def main():
         if args.part == "gemv":
             out = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
                    bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True),
+                   {"long_rows": [bench_w8a16(torch, R, gen, 1, N, K, read_yardstick=True) for N, K in LONG_ROWS]},
                    {"launch_floor": launch_floor(torch, R)}, {"read_fit": read_fit(torch, R)}]
         elif args.part == "qwen32b":
             out = [bench_qwen32b_quantize(torch, R, args.format, parity=not args.no_cpu)]
@@ -895,10 +900,11 @@ def main():
         extras["cool_down_s"] = cool_down(torch)
         extras["gemv_b1_llama8b"] = [bench_w8a16(torch, R, gen, 1, 14336, 4096, read_yardstick=True),
                                      bench_w8a16(torch, R, gen, 1, 4096, 14336, read_yardstick=True)]
+        extras["gemv_b1_long_rows"] = [bench_w8a16(torch, R, gen, 1, N, K, read_yardstick=True) for N, K in LONG_ROWS]
         extras["launch_floor"] = launch_floor(torch, R)
         extras["read_fit"] = read_fit(torch, R)
         log("gemv b1:", extras["gemv_b1_llama8b"], "launch floor:", extras["launch_floor"],
-            "read fit:", extras["read_fit"])
+            "read fit:", extras["read_fit"], "long rows:", extras["gemv_b1_long_rows"])
         extras["cool_down_s"] += cool_down(torch, 10.0)
         sk = []
         for M in (8, 64):
