@@ -825,9 +825,9 @@ int launch_gemv_rows_c(const uint16_t *x, const uint8_t *codes, const float *sca
 
 // Rows of 2..32 KB (1024 < K <= 32768: the activation's LDS copy is at most
 // 64 KB); the caller sends the rest to gemv_w8a16. Past 16 chunks the load
-// window is what keeps the rows in order: M = 1 [5120, 27648] 28.1 -> 23.2 us,
-// [3584, 19456] 13.4-14.0 -> 12.1 us against the strided walk (a plain read of
-// the codes 20.9 / 11.1 us).
+// window is what keeps the rows in order: M = 1 [5120, 27648] 27.9 -> 23.1-23.3
+// us, [3584, 18944] 13.6 -> 12.0 us against the strided walk (a plain read of
+// the codes 20.7 / 10.8 us).
 template <int F, int EPI = EPI_PLAIN>
 int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                      uint16_t *y, hipStream_t st, const float *res = nullptr, float *yres = nullptr) {

@@ -568,7 +568,10 @@ int launch_fp8_wide(const Fp8Args &g, hipStream_t st, uint32_t ldo = 0) {
 inline Fp8Args column_range(const Fp8Args &g, uint32_t n0, uint32_t n) {
     Fp8Args r = g;
     r.b = g.b + (size_t)n0 * g.K;
-    if (g.nsb > 1) r.sb = g.sb + n0, r.nsb = n;
+    if (g.nsb > 1) {   // one scale per weight row: those of the range
+        r.sb = g.sb + n0;
+        r.nsb = n;
+    }
     r.N = n;
     r.out = g.out + n0;
     return r;
