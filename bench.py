@@ -25,8 +25,9 @@ with no arithmetic, reng_hip_stream_narrow) beside the dominant quantize launch.
 
 The CPU baseline is the oracle (a C restatement of reng-fp8's quantizer: two
 passes, an IEEE divide per element, <= 8 threads by reng-fp8's split rule)
-timed on this host over layers 0-7 of the same set; those layers are also
-compared bit for bit with the GPU's codes and scales.
+timed on this host over layers 0-15 of the same set (about 4 s a run, the
+median of 3); those layers are also compared bit for bit with the GPU's codes
+and scales.
 
 roofline.traffic is the dominant quantize kernel's HBM bytes per launch from two
 rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE) that the default run starts as
@@ -216,7 +217,7 @@ def cpu_record(O, host, secs, what):
                        f"matrix with reng-fp8's split rule (<= 8 threads), {cpu_model()}, nproc {os.cpu_count()}")}
 
 
-def cpu_baseline_and_parity(torch, O, ws, fmt, layers=8):
+def cpu_baseline_and_parity(torch, O, ws, fmt, layers=16):
     import numpy as np
 
     sample = [m for m in ws.mats if m[0] < layers]
