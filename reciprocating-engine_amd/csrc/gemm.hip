@@ -1,7 +1,8 @@
 // gemm.hip - consumers of the quantizer's codes on CDNA4 (gfx950).
 //
-// 1. gemv_rows      (M = 1, 1024 < K <= 32768) and gemv_w8a16 (the other
-//                    M = 1, M = 2 with a short K, M <= 4 when K % 128 != 0):
+// 1. gemv_rows      (M = 1, 1024 < K <= 32768; M = 2, 1024 < K <= 8192) and
+//    gemv_w8a16     (the other M = 1, M = 2 with K <= 1024 or 8192 < K <=
+//                    16384, M <= 4 when K % 128 != 0):
 //                    y[m, n] = s[n] * sum_k x[m, k] * decode(c[n, k]); with
 //                    M = 1 gemv_w8a16 also has residual-add, SwiGLU-pair and
 //                    RoPE-pair epilogues and an RMSNorm prologue.
@@ -410,7 +411,13 @@ constexpr int GEMV_WINDOW = 10;
 // EPI_RESID (the decode step's projections that feed the residual stream)
 // writes f32 yres[n] = res[n] + bf16(y[n]) instead of y: gemv_w8a16's residual
 // epilogue on the same row sums, so the same bits.
-template <int F, int CPR, int WPB, int EPI = EPI_PLAIN>
+//
+// MR activation rows (1 or 2; x [MR, K], y [MR, N]): each wave still streams
+// one weight row, its chunks met by every activation row in LDS (MR x CPR x
+// 2 KB at most 64 KB), with the same lanes, order and accumulators per
+// activation row as for one, so an MR = 2 product equals two MR = 1 products
+// bit for bit.
+template <int F, int CPR, int WPB, int EPI = EPI_PLAIN, int MR = 1>
 // (No __restrict__ on the inputs: loads through a restrict pointer to const may
 // be treated as invariant and moved across the compiler barriers that fix the
 // issue order.)
@@ -419,22 +426,26 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *x, const u
                                                       uint16_t *__restrict__ y, const float *res,
                                                       float *__restrict__ yres) {
     static_assert(EPI == EPI_PLAIN || EPI == EPI_RESID, "plain or residual rows");
+    static_assert(MR == 1 || (MR == 2 && EPI == EPI_PLAIN), "two activation rows: plain output only");
+    static_assert(MR * CPR <= 32, "the activation's LDS copy is at most 64 KB");
     constexpr uint32_t XMAX = CPR * 128;                             // 16-byte activation pieces at most
     constexpr uint32_t XPT = (XMAX + 64 * WPB - 1) / (64 * WPB);     // pieces per thread
-    __shared__ __attribute__((aligned(16))) u32x4 xs[XMAX];
+    __shared__ __attribute__((aligned(16))) u32x4 xs[MR * XMAX];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t n = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nr = n < N ? n : N - 1;   // a wave past the last row reads row N - 1, stores nothing
-    const uint32_t xp = K / 8;               // 16-byte activation pieces
+    const uint32_t xp = K / 8;               // 16-byte activation pieces per row
     const uint32_t live = (K & 1023) ? (K & 1023) >> 4 : 64;   // lanes of the last chunk inside the row
     const float sv = scales ? scales[nr] : 1.0f;
     const u32x4 *x16 = reinterpret_cast<const u32x4 *>(x);
-    u32x4 xt[XPT];
+    u32x4 xt[MR][XPT];
 #pragma unroll
-    for (uint32_t j = 0; j < XPT; ++j) {
-        const uint32_t i = tid + j * 64 * WPB;
-        xt[j] = x16[i < xp ? i : xp - 1];
-    }
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (uint32_t j = 0; j < XPT; ++j) {
+            const uint32_t i = tid + j * 64 * WPB;
+            xt[r][j] = x16[r * xp + (i < xp ? i : xp - 1)];
+        }
     // The codes are requested after the scale and the activation.
     asm volatile("" ::: "memory");
     const u32x4 *wr = reinterpret_cast<const u32x4 *>(codes + (size_t)nr * K);
@@ -447,41 +458,53 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows(const uint16_t *x, const u
 #pragma unroll
     for (int c = 0; c < CPR && c < GEMV_WINDOW; ++c) request(c);
 #pragma unroll
-    for (uint32_t j = 0; j < XPT; ++j) {
-        const uint32_t i = tid + j * 64 * WPB;
-        if (i < xp) xs[i] = xt[j];
-    }
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (uint32_t j = 0; j < XPT; ++j) {
+            const uint32_t i = tid + j * 64 * WPB;
+            if (i < xp) xs[r * XMAX + i] = xt[r][j];
+        }
     lds_sync();
     // Past K in a ragged last chunk: no codes, and no activation past the LDS
     // copy either (a mask, not a branch, so the waits stay per chunk).
     const uint32_t keep_last = lane < live ? ~0u : 0u;
-    float a0 = 0.0f, a1 = 0.0f;
+    float a0[MR], a1[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) a0[r] = a1[r] = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
         if (c + GEMV_WINDOW < CPR) request(c + GEMV_WINDOW);
         uint32_t wv[8];
         decode16<F>(q[c], wv);
-        u32x4 xa = xs[128 * c + 2 * lane], xb = xs[128 * c + 2 * lane + 1];
         if (c == CPR - 1) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) wv[i] &= keep_last;
-            xa &= keep_last;
-            xb &= keep_last;
         }
-        a0 = dot2(wv[0], xa.x, a0);
-        a1 = dot2(wv[1], xa.y, a1);
-        a0 = dot2(wv[2], xa.z, a0);
-        a1 = dot2(wv[3], xa.w, a1);
-        a0 = dot2(wv[4], xb.x, a0);
-        a1 = dot2(wv[5], xb.y, a1);
-        a0 = dot2(wv[6], xb.z, a0);
-        a1 = dot2(wv[7], xb.w, a1);
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            u32x4 xa = xs[r * XMAX + 128 * c + 2 * lane], xb = xs[r * XMAX + 128 * c + 2 * lane + 1];
+            if (c == CPR - 1) {
+                xa &= keep_last;
+                xb &= keep_last;
+            }
+            a0[r] = dot2(wv[0], xa.x, a0[r]);
+            a1[r] = dot2(wv[1], xa.y, a1[r]);
+            a0[r] = dot2(wv[2], xa.z, a0[r]);
+            a1[r] = dot2(wv[3], xa.w, a1[r]);
+            a0[r] = dot2(wv[4], xb.x, a0[r]);
+            a1[r] = dot2(wv[5], xb.y, a1[r]);
+            a0[r] = dot2(wv[6], xb.z, a0[r]);
+            a1[r] = dot2(wv[7], xb.w, a1[r]);
+        }
     }
-    const float t = wave_sum_dpp(a0 + a1);
-    if (lane == 0 && n < N) {
-        const uint32_t b = f32_to_bf16_bits(t * sv);
-        if constexpr (EPI == EPI_RESID) yres[n] = res[n] + __uint_as_float(b << 16);
-        else y[n] = (uint16_t)b;
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        const float t = wave_sum_dpp(a0[r] + a1[r]);
+        if (lane == 0 && n < N) {
+            const uint32_t b = f32_to_bf16_bits(t * sv);
+            if constexpr (EPI == EPI_RESID) yres[n] = res[n] + __uint_as_float(b << 16);
+            else y[(size_t)r * N + n] = (uint16_t)b;
+        }
     }
 }
 
@@ -808,18 +831,18 @@ int launch_gemv_swiglu(const uint16_t *x, const uint8_t *codes, const float *sca
 // when there are more than 16 rows per CU, else 8-wave blocks (fewer copies
 // of a long activation per CU): [14336, 4096] 10.12 us with 4-wave blocks
 // against 10.25 with 8, [4096, 4096] 4.54 against 4.46.
-template <int F, int CPR, int EPI>
+template <int F, int CPR, int EPI, int MR>
 int launch_gemv_rows_c(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                        uint16_t *y, const float *res, float *yres, hipStream_t st) {
     if constexpr (CPR <= 8) {
         if (N > (uint32_t)device_props().cus * 16) {
-            hipLaunchKernelGGL((gemv_rows<F, CPR, 4, EPI>), dim3((N + 3) / 4), dim3(256), 0, st, x, codes, scales, N, K,
-                               y, res, yres);
+            hipLaunchKernelGGL((gemv_rows<F, CPR, 4, EPI, MR>), dim3((N + 3) / 4), dim3(256), 0, st, x, codes, scales,
+                               N, K, y, res, yres);
             return check_launch(EPI == EPI_RESID ? "gemv_rows (residual)" : "gemv_rows");
         }
     }
-    hipLaunchKernelGGL((gemv_rows<F, CPR, 8, EPI>), dim3((N + 7) / 8), dim3(512), 0, st, x, codes, scales, N, K, y,
-                       res, yres);
+    hipLaunchKernelGGL((gemv_rows<F, CPR, 8, EPI, MR>), dim3((N + 7) / 8), dim3(512), 0, st, x, codes, scales, N, K,
+                       y, res, yres);
     return check_launch(EPI == EPI_RESID ? "gemv_rows (residual)" : "gemv_rows");
 }
 
@@ -828,12 +851,14 @@ int launch_gemv_rows_c(const uint16_t *x, const uint8_t *codes, const float *sca
 // window is what keeps the rows in order: M = 1 [5120, 27648] 27.9 -> 23.1-23.3
 // us, [3584, 18944] 13.6 -> 12.0 us against the strided walk (a plain read of
 // the codes 20.7 / 10.8 us).
-template <int F, int EPI = EPI_PLAIN>
+template <int F, int EPI = EPI_PLAIN, int MR = 1>
 int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
                      uint16_t *y, hipStream_t st, const float *res = nullptr, float *yres = nullptr) {
     switch ((K + 1023) / 1024) {
-#define RENG_ROWS(C) \
-    case C: return launch_gemv_rows_c<F, C, EPI>(x, codes, scales, N, K, y, res, yres, st);
+#define RENG_ROWS(C)                                                                          \
+    case C:                                                                                   \
+        if constexpr (MR * C <= 32) return launch_gemv_rows_c<F, C, EPI, MR>(x, codes, scales, N, K, y, res, yres, st); \
+        break;
         RENG_ROWS(2) RENG_ROWS(3) RENG_ROWS(4) RENG_ROWS(5) RENG_ROWS(6) RENG_ROWS(7) RENG_ROWS(8) RENG_ROWS(9)
         RENG_ROWS(10) RENG_ROWS(11) RENG_ROWS(12) RENG_ROWS(13) RENG_ROWS(14) RENG_ROWS(15) RENG_ROWS(16)
         RENG_ROWS(17) RENG_ROWS(18) RENG_ROWS(19) RENG_ROWS(20) RENG_ROWS(21) RENG_ROWS(22) RENG_ROWS(23)
@@ -841,9 +866,10 @@ int launch_gemv_rows(const uint16_t *x, const uint8_t *codes, const float *scale
         RENG_ROWS(31) RENG_ROWS(32)
 #undef RENG_ROWS
         default:
-            set_error("gemv_rows: K = %u outside 1025..32768", K);
-            return RENG_HIP_EINVAL;
+            break;
     }
+    set_error("gemv_rows: K = %u outside 1025..%u for %d activation rows", K, 32768u / MR, MR);
+    return RENG_HIP_EINVAL;
 }
 
 int launch_gemv_residual(const uint16_t *x, const uint8_t *codes, const float *scales, uint32_t N, uint32_t K,
@@ -867,6 +893,12 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     // load window; x and codes are 16-byte aligned (checked by the entry point).
     if (M == 1 && K > 1024 && K <= 32768)
         return launch_gemv_rows<F>(x, codes, scales, N, K, y, st);
+    // Two rows of 1 to 8 KB: the same kernel with both rows in LDS (Llama
+    // [14336, 4096] 12.99 -> 11.56 us, Qwen2.5-7B [18944, 3584] 15.53 -> 12.9 us
+    // against the strided walk). Longer rows stay there: at [4096, 14336] the
+    // two 28 KB copies hold a CU to two blocks (13.65 against 13.02 us).
+    if (M == 2 && K > 1024 && K <= 8192)
+        return launch_gemv_rows<F, EPI_PLAIN, 2>(x, codes, scales, N, K, y, st);
     // More than 64 rows: output tiles on the bf16 MFMA, each code tile read
     // once per 64-256 activation rows (the 64-row loop below re-reads every
     // code once per 64 rows: M = 256 [14336, 4096] 86.8 -> 41.6 us).
@@ -888,7 +920,8 @@ int launch_w8a16_t(const uint16_t *x, const uint8_t *codes, const float *scales,
     // Three or four rows, or two once the activation outgrows the GEMV's LDS
     // copy: the MFMA kernel (activation rows padded to 8) is faster than the
     // GEMV's per-row dot products (Qwen2.5-7B [3584, 18944]: M = 3 26.3 ->
-    // 16.6 us, M = 2 22.5 -> 16.6 us; M = 2 with a short K stays on the GEMV).
+    // 16.6 us, M = 2 22.5 -> 16.6 us; M = 2 with K <= 8192 takes gemv_rows
+    // above, and up to 16384 the strided GEMV below).
     if (M >= 2 && M <= 4 && K % 128 == 0 && (M >= 3 || (size_t)M * K * 2 > 64 * 1024))
         return launch_skinny_mfma(x, codes, scales, M, N, K, F, y, st, fixed);
     if (M <= 4) {

@@ -172,13 +172,32 @@ def test_gemv_refuses_an_unaligned_activation(R):
 
 @pytest.mark.parametrize("M", [2, 3, 4])
 def test_gemv_small_batches(R, M):
-    """K % 128 != 0 keeps M <= 4 on the GEMV; with K % 128 == 0, M = 3 and 4
-    (and M = 2 at a long K) take the MFMA kernel with padded rows."""
+    """M = 2 with 1024 < K <= 8192 runs the one-wave-per-row GEMV with both
+    activation rows in LDS; otherwise K % 128 != 0 keeps M <= 4 on the strided
+    GEMV, and with K % 128 == 0, M = 3 and 4 (and M = 2 at a long K) take the
+    MFMA kernel with padded rows."""
     rng = np.random.default_rng(103 + M)
     check_w8a16(R, rng, M, 1024, 4096, E4M3)
     check_w8a16(R, rng, M, 1024, 4112, E4M3)
     check_w8a16(R, rng, M, 100, 176, E5M2)
     check_w8a16(R, rng, M, 300, 18944, E5M2)
+
+
+@pytest.mark.parametrize("N,K", [(1000, 4096), (333, 7184), (77, 8192), (5, 1040), (4101, 2048)])
+def test_gemv_two_rows_equal_two_single_rows(R, N, K):
+    """Two activation rows on the row GEMV (1024 < K <= 8192): each output row
+    is bit for bit the single-row GEMV of that activation row (same lanes, order
+    and accumulators per row), for ragged K, few rows, a partial last block, both
+    formats; and within the per-element bound of the oracle."""
+    rng = np.random.default_rng(N + 7 * K)
+    fmt = E4M3 if N % 2 else E5M2
+    q = quantized_weight(rng, N, K, fmt)
+    x = bf16_bits(rng.standard_normal((2, K)).astype(np.float32)).ravel()
+    y2 = bf16_out(R.gemm_w8a16(dev(x), dev(q.codes), dev(q.scales), 2, N, K, fmt)).reshape(2, N)
+    for r in range(2):
+        y1 = bf16_out(R.gemm_w8a16(dev(x[r * K:(r + 1) * K].copy()), dev(q.codes), dev(q.scales), 1, N, K, fmt))
+        assert np.array_equal(y2[r].view(np.uint32), y1.view(np.uint32)), (N, K, r)
+    assert_elementwise(y2, bf16_f32(x), q.dequantize().reshape(N, K), K, f"M=2 N={N} K={K}")
 
 
 @pytest.mark.parametrize("M", [1, 3])
