@@ -200,6 +200,37 @@ def test_gemv_two_rows_equal_two_single_rows(R, N, K):
     assert_elementwise(y2, bf16_f32(x), q.dequantize().reshape(N, K), K, f"M=2 N={N} K={K}")
 
 
+def random_w8a16_shapes(n=96, seed=20261202):
+    """Seeded (M, N, K, fmt) cases across the batch-size dispatch: M on and
+    around every boundary (1, 2, 3-4, 5-16, 17-64, > 64), K a multiple of 16
+    (half of them of 128, some past 8 and 16 KB rows), N from 1 up, sized so
+    the oracle finishes each in well under a second."""
+    rng = np.random.default_rng(seed)
+    ms = [1, 1, 2, 2, 3, 4, 5, 8, 9, 15, 16, 17, 24, 31, 32, 33, 48, 63, 64, 65, 96, 130]
+    out = []
+    while len(out) < n:
+        M = ms[len(out) % len(ms)]   # every M at least twice
+        K = int(rng.integers(1, 1250)) * 16
+        if rng.random() < 0.5:
+            K = max(128, K // 128 * 128)
+        if M <= 2 and rng.random() < 0.3:
+            K = int(rng.integers(1025, 2048)) * 16   # rows past 16 KB
+        N = int(rng.integers(1, 4000)) if rng.random() < 0.8 else int(rng.integers(1, 64))
+        if N * K > (16 << 20) or M * N * K > 1_000_000_000:
+            continue
+        out.append((M, N, K, E4M3 if rng.random() < 0.5 else E5M2))
+    return out
+
+
+@pytest.mark.parametrize("case", random_w8a16_shapes(), ids=lambda c: f"M{c[0]}-N{c[1]}-K{c[2]}-f{c[3]}")
+def test_w8a16_random_shapes(R, case):
+    """Every path of the batch-size dispatch on seeded random shapes, each
+    against the oracle (rel-L2) and float64 (per element)."""
+    M, N, K, fmt = case
+    rng = np.random.default_rng(M * 1_000_003 + N * 101 + K)
+    check_w8a16(R, rng, M, N, K, fmt, sample_cols=None if M * N <= 65536 else 512)
+
+
 @pytest.mark.parametrize("M", [1, 3])
 def test_gemv_many_rows_per_wave(R, M):
     """N = 300000 short rows: ~74 rows per wave, past the 64 per-row scales a
