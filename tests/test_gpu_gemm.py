@@ -567,6 +567,39 @@ def test_fp8_gemm_prefill_qwen_32b_shapes(R, shape):
     check_fp8(R, rng, 1024, N, K, E4M3, E4M3, sample_cols=192)
 
 
+def random_fp8_shapes(n=48, seed=20261203):
+    """Seeded fp8 x fp8 cases: M and N on and off every tile grid (whole tiles
+    take the wide forms, the rest the ragged kernel; 1024-row products with many
+    256-wide column tiles the mixed grid), K in 128-code stages, every format
+    pair and scale form."""
+    rng = np.random.default_rng(seed)
+    ms = [1, 7, 64, 100, 128, 256, 300, 512, 1000, 1024]
+    forms = [("pcs", "N"), ("unit", "N"), ("pcs", "1"), ("unit", "0"), ("pcs", "0")]
+    pairs = [(E4M3, E4M3), (E5M2, E5M2), (E4M3, E5M2), (E5M2, E4M3)]
+    out = []
+    while len(out) < n:
+        M = ms[len(out) % len(ms)]
+        K = 128 * int(rng.integers(1, 48))
+        r = rng.random()
+        N = 64 * int(rng.integers(1, 400)) if r < 0.4 else 256 * int(rng.integers(64, 112)) if r < 0.5 \
+            else int(rng.integers(1, 6000))
+        if M * N * K > 1_500_000_000:
+            continue
+        fa, fb = pairs[int(rng.integers(0, 4))]
+        act, nsb = forms[int(rng.integers(0, 5))]
+        out.append((M, N, K, fa, fb, act, nsb))
+    return out
+
+
+@pytest.mark.parametrize("case", random_fp8_shapes(), ids=lambda c: "M{}-N{}-K{}-{}x{}-{}-{}".format(*c))
+def test_fp8_gemm_random_shapes(R, case):
+    """The fp8 GEMM's dispatch on seeded random shapes, each against the oracle
+    (rel-L2) and float64 (per element, the fp8 bound)."""
+    M, N, K, fa, fb, act, nsb = case
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    check_fp8(R, rng, M, N, K, fa, fb, act, nsb, sample_cols=None if M * N <= 65536 else 256)
+
+
 @pytest.mark.parametrize("fmt", [E4M3, E5M2])
 def test_fp8_mfma_accumulation_over_k(R, fmt):
     """The fp8 MFMA's accumulation error against fp8_acc(K): codes drawn
