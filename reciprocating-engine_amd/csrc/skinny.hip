@@ -948,7 +948,8 @@ int launch_stage_copy(const uint16_t *x, const uint8_t *codes, uint32_t M, uint3
 // skinny_rows runs a product in one round of whole-K blocks; skinny_wide's
 // one-activation-tile form splits K over blocks and merges the splits in the
 // launch. The split form takes long rows (K >= 8192: Qwen2.5-7B down
-// [3584, 18944] at M = 8 17.9 -> 15.0 us, M = 16 22.3 -> 15.0 us), and for
+// [3584, 18944] at M = 8 17.9 -> 15.0 us, M = 16 22.3 -> 15.0 us; at M <= 8
+// not where 16-row tiles fill the CUs, below), and for
 // 8 < M <= 16 every product but those whose 16-row tiles fill between half
 // and all of the CUs ([3584, 3584]: 6.5 against 6.9 us; kv [512, 3584]
 // 5.6 -> 5.1 us, gate/up [18944, 3584] 21.5 -> 17.5 us).
@@ -956,7 +957,13 @@ int launch_skinny_mfma(const uint16_t *x, const uint8_t *codes, const float *sca
                        uint32_t K, int format, uint16_t *y, hipStream_t st, const SplitScratch *fixed) {
     using namespace skinny;
     const uint32_t cus = (uint32_t)device_props().cus, t16 = (N + 15) / 16;
-    const bool split = K >= 8192 || (M > 8 && !(t16 <= cus && 2 * t16 > cus));
+    // Long rows stay whole-K at M <= 8 where skinny_rows' one 16-row tile per
+    // workgroup keeps (nearly) every CU busy: Llama-3.1-8B down [4096, 14336]
+    // M = 8 13.8 -> 13.0 us, M = 4 13.9 -> 11.9 us, [4096, 8192] M = 8 10.8 ->
+    // 8.7 us; not with CUs idle (Qwen2.5-7B down, 224 tiles: 16.0 against 14.9
+    // us) nor at M = 16 (15.9 against 13.8 us).
+    const bool full16 = M <= 8 && t16 <= cus && 16 * t16 >= 15 * cus;
+    const bool split = (K >= 8192 && !full16) || (M > 8 && !(t16 <= cus && 2 * t16 > cus));
     if (split) {
         if (format == RENG_HIP_E4M3) return launch_wide_mt<RENG_HIP_E4M3, 1>(x, codes, scales, M, N, K, y, st, fixed);
         return launch_wide_mt<RENG_HIP_E5M2, 1>(x, codes, scales, M, N, K, y, st, fixed);

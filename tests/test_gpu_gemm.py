@@ -305,9 +305,11 @@ def test_short_last_chunk_is_deterministic(R, M, N, K):
 # for M <= 8 and K <= 4096: N = 20000, and 18950 at that K limit), K runs with
 # a one-chunk last stage (K % 256 == 128), K shorter than the waves' split
 # (some waves get no chunk), N not a multiple of 16 or of 4, and both
-# staged-activation heights (8 and 16 rows).
+# staged-activation heights (8 and 16 rows); and long rows whose 16-row tiles
+# fill the CUs (N = 4096 and 3900 at K = 14336 and 8192: whole-K at M <= 8).
 @pytest.mark.parametrize("M", [5, 7, 8, 9, 12, 16])
-@pytest.mark.parametrize("N,K", [(200, 128), (4101, 384), (8000, 256), (16000, 3712), (20000, 1152), (18950, 4096)])
+@pytest.mark.parametrize("N,K", [(200, 128), (4101, 384), (8000, 256), (16000, 3712), (20000, 1152), (18950, 4096),
+                                 (4096, 14336), (3900, 8192)])
 def test_skinny_rows_block_shapes(R, M, N, K):
     rng = np.random.default_rng(1000 * M + N + K)
     fmt = E4M3 if (M + N) % 2 else E5M2
