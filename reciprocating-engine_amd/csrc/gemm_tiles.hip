@@ -319,7 +319,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_tiles(const uint16_t *__
             const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + r * RB + slot(r, c) * 16);
             uint16_t *dst = y + (size_t)m * N + nc;
             if (vec_out && nc + 8 <= N) {
-                *reinterpret_cast<u32x4 *>(dst) = v;
+                // Non-temporal, as the fp8 GEMM's epilogue (same-box A/B: equal or
+                // 0.5-2.5% faster on every tile form's product, M = 256 [14336,
+                // 4096] 39.5 -> 38.9 us).
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(dst));
             } else {
                 const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
